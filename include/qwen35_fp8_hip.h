@@ -1,0 +1,224 @@
+/*
+ * libqwen35_fp8_hip.so -- MI355X (gfx950) batch-1 FP8 decode path for
+ * Qwen3.5-shaped hybrid models.
+ *
+ * Conventions (all entry points):
+ *   - pointers are device pointers owned by the caller; activations are bf16
+ *     (uint16 bit patterns), weights E4M3FN bytes, norm weights fp32 unless
+ *     stated, GatedDeltaNet norm weight bf16;
+ *   - `stream` is a hipStream_t (the reference passed cudaStream_t); launches
+ *     are asynchronous on it;
+ *   - scale-mode code `kb` (the reference's `K_blocks`): kb > 1 -> 128x128
+ *     block scales [ceil(N/128), kb]; kb == 1 -> one scale per row [N];
+ *     kb < 0 -> per-row-per-block [N, -kb].
+ *
+ * Section 1 re-exports the reference's ctypes ABI with identical names,
+ * argument order and meaning (bf16 scale_inv, void return).  Section 2 holds
+ * the native entry points (fp32 scale_inv, int status: 0 ok, -1 error with
+ * qh_last_error()).
+ */
+#ifndef QWEN35_FP8_HIP_H
+#define QWEN35_FP8_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* qh_stream_t; /* hipStream_t */
+
+/* ========================= 1. reference ABI (bf16 scales) ================= */
+
+/* replaces fp8_gemm_batch, qwen3_infer/csrc/fp8_kernels.cu:72-89 (bound at main.py:108) */
+void fp8_gemm_batch(const void* x_bf16, const void* w_fp8, const void* w_scale_bf16, void* y_bf16,
+                    int M, int N, int K, int K_blocks, qh_stream_t stream);
+
+/* replaces launch_gemv_v4_extern, fused_kernels.cu:1328-1336 (main.py:119) */
+void launch_gemv_v4_extern(const void* x, const void* w, const void* s, void* y, int N, int K,
+                           int K_blk, qh_stream_t stream);
+
+/* replaces launch_gemv_v3_extern, fused_kernels.cu:981-989 (same kernel as v4 here) */
+void launch_gemv_v3_extern(const void* x, const void* w, const void* s, void* y, int N, int K,
+                           int K_blk, qh_stream_t stream);
+
+/* replaces launch_linear_in_proj4, fused_kernels.cu:1338-1354 (main.py:123-132) */
+void launch_linear_in_proj4(const void* x, const void* w0, const void* s0, void* y0, int n0,
+                            int kb0, const void* w1, const void* s1, void* y1, int n1, int kb1,
+                            const void* w2, const void* s2, void* y2, int n2, int kb2,
+                            const void* w3, const void* s3, void* y3, int n3, int kb3, int K,
+                            qh_stream_t stream);
+
+/* replaces launch_fused_qkv, fused_kernels.cu:991-1007 (main.py:133-140) */
+void launch_fused_qkv(const void* x, const void* w_q, const void* w_k, const void* w_v,
+                      const void* s_q, const void* s_k, const void* s_v, void* q_out, void* k_out,
+                      void* v_out, int K, int N_q, int N_k, int N_v, int K_blk, int N_q_blk,
+                      int N_k_blk, int N_v_blk, qh_stream_t stream);
+
+/* replaces launch_fused_gate_up, fused_kernels.cu:1009-1025 (main.py:141-148) */
+void launch_fused_gate_up(const void* x, const void* w_gate, const void* w_up, const void* s_gate,
+                          const void* s_up, void* gate_out, void* up_out, int K, int N_gate,
+                          int N_up, int K_blk, int N_gate_blk, int N_up_blk, qh_stream_t stream);
+
+/* replaces launch_rmsnorm_ip, fused_kernels.cu:1055-1062 (main.py:149-153) */
+void launch_rmsnorm_ip(void* x, const void* weight, int N, int D, float eps, qh_stream_t stream);
+
+/* replaces launch_rmsnorm_out, fused_kernels.cu:1045-1053 (main.py:154-162) */
+void launch_rmsnorm_out(const void* x, const void* weight, void* out, int N, int D, float eps,
+                        qh_stream_t stream);
+
+/* replaces launch_fused_attn, fused_kernels.cu:1027-1043 (main.py:168-172) */
+void launch_fused_attn(const void* q, const void* k_cache, const void* v_cache, void* output,
+                       int seq_len, int max_seq_len, int head_dim, int n_heads, int n_kv_heads,
+                       qh_stream_t stream);
+
+/* replaces launch_fused_attn_v2, fused_kernels.cu:1300-1326 (main.py:163-167) */
+void launch_fused_attn_v2(const void* q, const void* k_cache, const void* v_cache, void* output,
+                          int seq_len, int max_seq_len, int head_dim, int n_heads, int n_kv_heads,
+                          qh_stream_t stream);
+
+/* replaces layer_pre_attn, fused_kernels.cu:1066-1091 (main.py:184-193) */
+void layer_pre_attn(const void* hidden, const float* norm_weight, const void* w_q, const void* s_q,
+                    int N_q, int N_q_blk, const void* w_k, const void* s_k, int N_k, int N_k_blk,
+                    const void* w_v, const void* s_v, int N_v, int N_v_blk, void* q_out,
+                    void* k_out, void* v_out, void* norm_ws, int h_dim, int K_blk,
+                    qh_stream_t stream);
+
+/* replaces layer_post_attn, fused_kernels.cu:1102-1150 (main.py:194-206) */
+void layer_post_attn(const void* hidden, const void* attn_out, const void* w_o, const void* s_o,
+                     int N_o, int N_o_blk, const float* norm_weight, const void* w_g,
+                     const void* s_g, int N_g, int N_g_blk, const void* w_u, const void* s_u,
+                     int N_u, int N_u_blk, const void* w_d, const void* s_d, int N_d, int N_d_blk,
+                     void* output, void* ws, void* gate_buf, void* up_buf, void* silu_buf,
+                     int h_dim, int attn_dim, int K_blk_o, int K_blk_gu, int K_blk_d,
+                     qh_stream_t stream);
+
+/* replaces layer_post_o_fp8_mlp, fused_kernels.cu:1156-1195 (main.py:207-217) */
+void layer_post_o_fp8_mlp(const void* hidden, const void* o_out, const float* norm_weight,
+                          const void* w_g, const void* s_g, int N_g, const void* w_u,
+                          const void* s_u, int N_u, const void* w_d, const void* s_d, int N_d,
+                          void* output, void* ws, void* gate_buf, void* up_buf, void* silu_buf,
+                          int h_dim, int K_blk_gu, int K_blk_d, qh_stream_t stream);
+
+/* replaces layer_mid_attn, fused_kernels.cu:1224-1297 (main.py:173-183) */
+void layer_mid_attn(void* q_buf, void* k_buf, const void* v_buf, void* attn_out,
+                    const float* q_norm_weight, const float* k_norm_weight,
+                    const float* cos_table, const float* sin_table, void* k_cache, void* v_cache,
+                    int pos, int past_len, int total_seq, int max_seq_len, int head_dim,
+                    int rotary_dim, int n_heads, int n_kv_heads, qh_stream_t stream);
+
+/* replaces launch_prepare_linear_gates, fused_kernels.cu:942-954 (main.py:218-225) */
+void launch_prepare_linear_gates(const void* a, const void* beta_in, const float* A_log,
+                                 const float* dt_bias, void* g_out, void* beta_out, int heads,
+                                 qh_stream_t stream);
+
+/* replaces launch_rmsnorm_gated_decode, fused_kernels.cu:956-965 (main.py:226-229) */
+void launch_rmsnorm_gated_decode(const void* core, const void* z, const void* weight, void* out,
+                                 int heads, int head_dim, float eps, qh_stream_t stream);
+
+/* replaces launch_delta_rule_decode, fused_kernels.cu:967-979 (main.py:231-240) */
+void launch_delta_rule_decode(const void* q, const void* k, const void* v, const void* g,
+                              const void* beta, void* state, void* output, int n_heads,
+                              int head_dim, qh_stream_t stream);
+
+/* ========================= 2. native entry points (fp32 scales) ============ */
+
+/* Last error message of the calling thread (no reference counterpart: the
+ * reference kernels have no error channel). */
+const char* qh_last_error(void);
+void qh_clear_error(void);
+int qh_abi_version(void);
+
+/* Grouped block-scaled GEMV, up to 4 segments sharing x (generalises
+ * launch_gemv_v4_extern / launch_linear_in_proj4 / launch_fused_qkv).
+ * Prologue: x := bf16(x + x2) if x2; x := (1+w) RMSNorm(x) if norm_w.
+ * Epilogue (nseg == 1): y := bf16(res + bf16(Wx)), res = res1 or bf16(res1+res2).
+ * scales_bf16 selects bf16 scale_inv (reference format) instead of fp32. */
+int qh_gemv_e4m3(const void* x, const void* x2, const float* norm_w, float eps, int K,
+                 const void* res1, const void* res2, int nseg, const void* w0, const void* s0,
+                 void* y0, int n0, int kb0, const void* w1, const void* s1, void* y1, int n1,
+                 int kb1, const void* w2, const void* s2, void* y2, int n2, int kb2,
+                 const void* w3, const void* s3, void* y3, int n3, int kb3, int scales_bf16,
+                 qh_stream_t stream);
+
+/* Paired gate/up GEMV, optional add + (1+w) RMSNorm prologue, SiLU(g)*u
+ * epilogue on fp32 accumulators (fused_kernels.cu:398-479 semantics). */
+int qh_mlp_gate_up(const void* x, const void* x2, const float* norm_w, float eps, int K,
+                   const void* w_g, const void* s_g, const void* w_u, const void* s_u, int N,
+                   int kb, void* m_out, void* g_out, void* u_out, int scales_bf16,
+                   qh_stream_t stream);
+
+/* Decode MLP block: h2 = bf16(h + o); out = bf16(h2 + down(silu(gate)*up of
+ * RMSNorm(h2))) (layer_post_o_fp8_mlp semantics, fp32 scales). */
+int qh_mlp_decode(const void* h, const void* o, const float* norm_w, float eps, int H,
+                  const void* w_g, const void* s_g, const void* w_u, const void* s_u, int I,
+                  int kb_gu, const void* w_d, const void* s_d, int kb_d, void* m_buf, void* out,
+                  int scales_bf16, qh_stream_t stream);
+
+/* (1+w) RMSNorm of `rows` rows of D (out may equal x). */
+int qh_rmsnorm(const void* x, const float* w, void* out, int rows, int D, float eps,
+               qh_stream_t stream);
+
+/* Scratch bytes for qh_attn_decode with nsplit > 1. */
+size_t qh_attn_scratch_bytes(int n_kv_heads, int nsplit, int head_dim);
+
+/* Full-attention decode (layer_mid_attn + the sigmoid output gate of
+ * main.py:1059): q/k head RMSNorm, partial RoPE, KV write, split-K GQA
+ * attention.  Position t = *pos_dev (device) if pos_dev else pos. */
+int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_stride,
+                   const void* k_new, const void* v_new, const float* q_norm_w,
+                   const float* k_norm_w, const float* cos_t, const float* sin_t, void* k_cache,
+                   void* v_cache, int max_seq, int head_dim, int rot, int n_heads, int n_kv,
+                   const int* pos_dev, int pos, int nsplit, void* scratch, unsigned* counters,
+                   void* out, float eps, qh_stream_t stream);
+
+/* GatedDeltaNet decode step: causal conv update (4-slot ring indexed by
+ * position), gates, l2norm, delta rule (state in place), gated RMSNorm
+ * (main.py:1064-1162 with launch_delta_rule_decode semantics). */
+int qh_gdn_decode(const void* mixed, const void* a, const void* b, const void* z,
+                  void* conv_ring, const void* conv_w, const float* A_log, const float* dt_bias,
+                  const void* norm_w, float* state, void* core, void* out, unsigned* counters,
+                  const int* pos_dev, int pos, int Hk, int Hv, int dk, int dv, float eps,
+                  qh_stream_t stream);
+
+/* Scratch bytes for qh_lm_head_argmax. */
+size_t qh_lm_head_scratch_bytes(int N);
+
+/* bf16 lm_head GEMV (F.linear, main.py:1600-1601) with the fused final RMSNorm
+ * and greedy argmax (lowest index on ties); optional token history, position
+ * increment and next-token embedding gather. */
+int qh_lm_head_argmax(const void* x, const float* norm_w, float eps, int K, const void* w, int N,
+                      void* logits, void* scratch, unsigned* counter, int64_t* tok_out,
+                      int64_t* tok_hist, int hist_len, int* pos_dev, const void* embed,
+                      void* embed_out, qh_stream_t stream);
+
+/* Embedding row gather (F.embedding, main.py:1587); ids outside [0, vocab)
+ * give a zero row. */
+int qh_embed(const void* table, const int64_t* ids, void* out, int n, int K, int vocab,
+             qh_stream_t stream);
+
+/* bf16 elementwise add (elem_add_kernel, fused_kernels.cu:553-559). */
+int qh_add_bf16(const void* a, const void* b, void* out, int n, qh_stream_t stream);
+
+/* GatedDeltaNet gates (launch_prepare_linear_gates semantics, torch softplus). */
+int qh_linear_gates(const void* a, const void* b, const float* A_log, const float* dt_bias,
+                    float* g_out, void* beta_out, int heads, qh_stream_t stream);
+
+/* Gated RMSNorm per head; bf16_steps=1 follows main.py:1152-1158, 0 the
+ * fused kernel fused_kernels.cu:592-618. */
+int qh_gated_rmsnorm(const void* core, const void* z, const void* w, void* out, int heads,
+                     int head_dim, float eps, int bf16_steps, qh_stream_t stream);
+
+/* Workspace bytes for qh_gemm_e4m3. */
+size_t qh_gemm_workspace_size(int M, int K);
+
+/* Prefill GEMM on the fp8 matrix cores (fp8_gemm_batch semantics). */
+int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
+                 int kb, int scales_bf16, void* ws, qh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN35_FP8_HIP_H */

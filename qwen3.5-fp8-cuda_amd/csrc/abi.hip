@@ -1,0 +1,608 @@
+// C-ABI of libqwen35_fp8_hip.so.
+//
+// Two families of entry points, all declared in include/qwen35_fp8_hip.h:
+//   1. The reference engine's ctypes ABI (same names, argument order and
+//      meaning as qwen3_infer/csrc/fused_kernels.cu:940-1356 and
+//      fp8_kernels.cu:68-91): bf16 scale_inv, `void` return, stream last.
+//      Invalid arguments launch nothing and record a message for
+//      qh_last_error() (the reference silently launches garbage or no-ops).
+//   2. Native `qh_*` entry points used by this framework's host: fp32
+//      scale_inv, device-resident positions for HIP-graph replay, fused
+//      epilogues; they return 0 on success and -1 with qh_last_error() set.
+// Every buffer is caller-owned device memory.  The one exception is the
+// reference's fp8_gemm_batch, which passes no workspace: the prefill GEMM then
+// keeps one internal, grow-on-demand activation buffer (gemm.hip).
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "qh_attn.h"
+#include "qh_gdn.h"
+#include "qh_gemm.h"
+#include "qh_kernels.h"
+#include "qh_norm.h"
+
+#define QH_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+thread_local char g_err[512] = "";
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    qh_set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return -1;
+  }
+  return 0;
+}
+
+bool k_ok(int K, const char* what) {
+  if (K <= 0 || (K % 8) != 0) {
+    qh_set_error("%s: K=%d must be a positive multiple of 8", what, K);
+    return false;
+  }
+  return true;
+}
+
+QhGemvSeg seg(const void* w, const void* s, void* y, int n, int kb) {
+  QhGemvSeg g;
+  g.w = (const uint8_t*)w;
+  g.s = s;
+  g.y = (uint16_t*)y;
+  g.n = n;
+  g.kb = kb;
+  return g;
+}
+
+QhGemvParams gemv_params(const void* x, int K) {
+  QhGemvParams p;
+  memset(&p, 0, sizeof(p));
+  p.x = (const uint16_t*)x;
+  p.K = K;
+  p.eps = 1e-6f;
+  return p;
+}
+
+int run_gemv(QhGemvParams& p, bool bf16_scales, const char* what, hipStream_t st) {
+  if (!k_ok(p.K, what)) return -1;
+  for (int i = 0; i < p.nseg; ++i) {
+    if (p.seg[i].n < 0 || (p.seg[i].n > 0 && (!p.seg[i].w || !p.seg[i].s || !p.seg[i].y))) {
+      qh_set_error("%s: segment %d has null pointers or negative rows", what, i);
+      return -1;
+    }
+  }
+  if (qh_launch_gemv(p, bf16_scales, st) != 0) return -1;
+  return check_launch(what);
+}
+
+}  // namespace
+
+void qh_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+// ============================================================================
+// Library info
+// ============================================================================
+QH_EXPORT const char* qh_last_error(void) { return g_err; }
+QH_EXPORT void qh_clear_error(void) { g_err[0] = '\0'; }
+QH_EXPORT int qh_abi_version(void) { return 1; }
+
+// ============================================================================
+// Reference ABI (bf16 scales)
+// ============================================================================
+QH_EXPORT void launch_gemv_v4_extern(const void* x, const void* w, const void* s, void* y, int N,
+                                     int K, int K_blk, hipStream_t stream) {
+  QhGemvParams p = gemv_params(x, K);
+  p.nseg = 1;
+  p.seg[0] = seg(w, s, y, N, K_blk);
+  run_gemv(p, true, "launch_gemv_v4_extern", stream);
+}
+
+QH_EXPORT void launch_gemv_v3_extern(const void* x, const void* w, const void* s, void* y, int N,
+                                     int K, int K_blk, hipStream_t stream) {
+  launch_gemv_v4_extern(x, w, s, y, N, K, K_blk, stream);
+}
+
+QH_EXPORT void launch_linear_in_proj4(const void* x, const void* w0, const void* s0, void* y0,
+                                      int n0, int kb0, const void* w1, const void* s1, void* y1,
+                                      int n1, int kb1, const void* w2, const void* s2, void* y2,
+                                      int n2, int kb2, const void* w3, const void* s3, void* y3,
+                                      int n3, int kb3, int K, hipStream_t stream) {
+  QhGemvParams p = gemv_params(x, K);
+  p.nseg = 4;
+  p.seg[0] = seg(w0, s0, y0, n0, kb0);
+  p.seg[1] = seg(w1, s1, y1, n1, kb1);
+  p.seg[2] = seg(w2, s2, y2, n2, kb2);
+  p.seg[3] = seg(w3, s3, y3, n3, kb3);
+  run_gemv(p, true, "launch_linear_in_proj4", stream);
+}
+
+QH_EXPORT void launch_fused_qkv(const void* x, const void* w_q, const void* w_k, const void* w_v,
+                                const void* s_q, const void* s_k, const void* s_v, void* q_out,
+                                void* k_out, void* v_out, int K, int N_q, int N_k, int N_v,
+                                int K_blk, int N_q_blk, int N_k_blk, int N_v_blk,
+                                hipStream_t stream) {
+  (void)N_q_blk; (void)N_k_blk; (void)N_v_blk;  // unused by the reference kernel too
+  QhGemvParams p = gemv_params(x, K);
+  p.nseg = 3;
+  p.seg[0] = seg(w_q, s_q, q_out, N_q, K_blk);
+  p.seg[1] = seg(w_k, s_k, k_out, N_k, K_blk);
+  p.seg[2] = seg(w_v, s_v, v_out, N_v, K_blk);
+  run_gemv(p, true, "launch_fused_qkv", stream);
+}
+
+QH_EXPORT void launch_fused_gate_up(const void* x, const void* w_gate, const void* w_up,
+                                    const void* s_gate, const void* s_up, void* gate_out,
+                                    void* up_out, int K, int N_gate, int N_up, int K_blk,
+                                    int N_gate_blk, int N_up_blk, hipStream_t stream) {
+  (void)N_gate_blk; (void)N_up_blk;
+  QhGemvParams p = gemv_params(x, K);
+  p.nseg = 2;
+  p.seg[0] = seg(w_gate, s_gate, gate_out, N_gate, K_blk);
+  p.seg[1] = seg(w_up, s_up, up_out, N_up, K_blk);
+  run_gemv(p, true, "launch_fused_gate_up", stream);
+}
+
+QH_EXPORT void launch_rmsnorm_ip(void* x, const void* weight, int N, int D, float eps,
+                                 hipStream_t stream) {
+  if (N < 0 || D <= 0) {
+    qh_set_error("launch_rmsnorm_ip: bad shape N=%d D=%d", N, D);
+    return;
+  }
+  qh_launch_rmsnorm_rows(x, (const float*)weight, x, N, D, eps, stream);
+  check_launch("launch_rmsnorm_ip");
+}
+
+QH_EXPORT void launch_rmsnorm_out(const void* x, const void* weight, void* out, int N, int D,
+                                  float eps, hipStream_t stream) {
+  if (N < 0 || D <= 0) {
+    qh_set_error("launch_rmsnorm_out: bad shape N=%d D=%d", N, D);
+    return;
+  }
+  qh_launch_rmsnorm_rows(x, (const float*)weight, out, N, D, eps, stream);
+  check_launch("launch_rmsnorm_out");
+}
+
+static void attn_only(const char* what, const void* q, const void* k_cache, const void* v_cache,
+                      void* output, int seq_len, int max_seq_len, int head_dim, int n_heads,
+                      int n_kv_heads, hipStream_t stream) {
+  QhAttnParams a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q;
+  a.q_stride = head_dim;
+  a.k_cache = (uint16_t*)k_cache;
+  a.v_cache = (uint16_t*)v_cache;
+  a.max_seq = max_seq_len;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.rope_pos = 0;
+  a.slot = 0;  // no new token (k_new is null): nothing is written
+  a.total = seq_len;
+  a.nsplit = 1;
+  a.out = (uint16_t*)output;
+  a.eps = 1e-6f;
+  if (seq_len < 1 || seq_len > max_seq_len) {
+    qh_set_error("%s: seq_len=%d out of range (max %d)", what, seq_len, max_seq_len);
+    return;
+  }
+  if (qh_launch_attn(a, head_dim, stream) == 0) check_launch(what);
+}
+
+QH_EXPORT void launch_fused_attn(const void* q, const void* k_cache, const void* v_cache,
+                                 void* output, int seq_len, int max_seq_len, int head_dim,
+                                 int n_heads, int n_kv_heads, hipStream_t stream) {
+  attn_only("launch_fused_attn", q, k_cache, v_cache, output, seq_len, max_seq_len, head_dim,
+            n_heads, n_kv_heads, stream);
+}
+
+QH_EXPORT void launch_fused_attn_v2(const void* q, const void* k_cache, const void* v_cache,
+                                    void* output, int seq_len, int max_seq_len, int head_dim,
+                                    int n_heads, int n_kv_heads, hipStream_t stream) {
+  attn_only("launch_fused_attn_v2", q, k_cache, v_cache, output, seq_len, max_seq_len, head_dim,
+            n_heads, n_kv_heads, stream);
+}
+
+QH_EXPORT void layer_pre_attn(const void* hidden, const float* norm_weight, const void* w_q,
+                              const void* s_q, int N_q, int N_q_blk, const void* w_k,
+                              const void* s_k, int N_k, int N_k_blk, const void* w_v,
+                              const void* s_v, int N_v, int N_v_blk, void* q_out, void* k_out,
+                              void* v_out, void* norm_ws, int h_dim, int K_blk,
+                              hipStream_t stream) {
+  (void)N_q_blk; (void)N_k_blk; (void)N_v_blk;
+  qh_launch_rmsnorm_rows(hidden, norm_weight, norm_ws, 1, h_dim, 1e-6f, stream);
+  launch_fused_qkv(norm_ws, w_q, w_k, w_v, s_q, s_k, s_v, q_out, k_out, v_out, h_dim, N_q, N_k,
+                   N_v, K_blk, 0, 0, 0, stream);
+}
+
+QH_EXPORT void layer_post_o_fp8_mlp(const void* hidden, const void* o_out,
+                                    const float* norm_weight, const void* w_g, const void* s_g,
+                                    int N_g, const void* w_u, const void* s_u, int N_u,
+                                    const void* w_d, const void* s_d, int N_d, void* output,
+                                    void* ws, void* gate_buf, void* up_buf, void* silu_buf,
+                                    int h_dim, int K_blk_gu, int K_blk_d, hipStream_t stream) {
+  (void)ws;
+  if (N_g != N_u || !k_ok(h_dim, "layer_post_o_fp8_mlp") || !k_ok(N_g, "layer_post_o_fp8_mlp"))
+    return;
+  QhMlpParams m;
+  memset(&m, 0, sizeof(m));
+  m.x = (const uint16_t*)hidden;
+  m.x2 = (const uint16_t*)o_out;
+  m.norm_w = norm_weight;
+  m.eps = 1e-6f;
+  m.K = h_dim;
+  m.wg = (const uint8_t*)w_g;
+  m.sg = s_g;
+  m.wu = (const uint8_t*)w_u;
+  m.su = s_u;
+  m.N = N_g;
+  m.kb = K_blk_gu;
+  m.m_out = (uint16_t*)silu_buf;
+  m.g_out = (uint16_t*)gate_buf;
+  m.u_out = (uint16_t*)up_buf;
+  if (qh_launch_mlp(m, true, stream) != 0 || check_launch("layer_post_o_fp8_mlp") != 0) return;
+  QhGemvParams p = gemv_params(silu_buf, N_g);
+  p.nseg = 1;
+  p.seg[0] = seg(w_d, s_d, output, N_d, K_blk_d);
+  p.res1 = (const uint16_t*)hidden;
+  p.res2 = (const uint16_t*)o_out;
+  run_gemv(p, true, "layer_post_o_fp8_mlp", stream);
+}
+
+QH_EXPORT void layer_post_attn(const void* hidden, const void* attn_out, const void* w_o,
+                               const void* s_o, int N_o, int N_o_blk, const float* norm_weight,
+                               const void* w_g, const void* s_g, int N_g, int N_g_blk,
+                               const void* w_u, const void* s_u, int N_u, int N_u_blk,
+                               const void* w_d, const void* s_d, int N_d, int N_d_blk,
+                               void* output, void* ws, void* gate_buf, void* up_buf,
+                               void* silu_buf, int h_dim, int attn_dim, int K_blk_o, int K_blk_gu,
+                               int K_blk_d, hipStream_t stream) {
+  (void)N_o_blk; (void)N_g_blk; (void)N_u_blk; (void)N_d_blk; (void)ws;
+  if (N_o != h_dim) {
+    qh_set_error("layer_post_attn: N_o=%d must equal h_dim=%d", N_o, h_dim);
+    return;
+  }
+  // output = bf16(hidden + bf16(W_o attn_out))
+  QhGemvParams p = gemv_params(attn_out, attn_dim);
+  p.nseg = 1;
+  p.seg[0] = seg(w_o, s_o, output, N_o, K_blk_o);
+  p.res1 = (const uint16_t*)hidden;
+  if (run_gemv(p, true, "layer_post_attn", stream) != 0) return;
+  if (N_g != N_u || !k_ok(N_g, "layer_post_attn")) return;
+  QhMlpParams m;
+  memset(&m, 0, sizeof(m));
+  m.x = (const uint16_t*)output;
+  m.norm_w = norm_weight;
+  m.eps = 1e-6f;
+  m.K = h_dim;
+  m.wg = (const uint8_t*)w_g;
+  m.sg = s_g;
+  m.wu = (const uint8_t*)w_u;
+  m.su = s_u;
+  m.N = N_g;
+  m.kb = K_blk_gu;
+  m.m_out = (uint16_t*)silu_buf;
+  m.g_out = (uint16_t*)gate_buf;
+  m.u_out = (uint16_t*)up_buf;
+  if (qh_launch_mlp(m, true, stream) != 0 || check_launch("layer_post_attn") != 0) return;
+  QhGemvParams d = gemv_params(silu_buf, N_g);
+  d.nseg = 1;
+  d.seg[0] = seg(w_d, s_d, output, N_d, K_blk_d);
+  d.res1 = (const uint16_t*)output;
+  run_gemv(d, true, "layer_post_attn", stream);
+}
+
+QH_EXPORT void layer_mid_attn(void* q_buf, void* k_buf, const void* v_buf, void* attn_out,
+                              const float* q_norm_weight, const float* k_norm_weight,
+                              const float* cos_table, const float* sin_table, void* k_cache,
+                              void* v_cache, int pos, int past_len, int total_seq,
+                              int max_seq_len, int head_dim, int rotary_dim, int n_heads,
+                              int n_kv_heads, hipStream_t stream) {
+  QhAttnParams a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q_buf;
+  a.q_stride = head_dim;
+  a.k_new = (const uint16_t*)k_buf;
+  a.v_new = (const uint16_t*)v_buf;
+  a.q_wb = (uint16_t*)q_buf;
+  a.k_wb = (uint16_t*)k_buf;
+  a.q_norm_w = q_norm_weight;
+  a.k_norm_w = k_norm_weight;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.k_cache = (uint16_t*)k_cache;
+  a.v_cache = (uint16_t*)v_cache;
+  a.max_seq = max_seq_len;
+  a.rot = rotary_dim;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv_heads;
+  a.rope_pos = pos;
+  a.slot = past_len;
+  a.total = total_seq;
+  a.nsplit = 1;
+  a.out = (uint16_t*)attn_out;
+  a.eps = 1e-6f;
+  if (qh_launch_attn(a, head_dim, stream) == 0) check_launch("layer_mid_attn");
+}
+
+QH_EXPORT void launch_prepare_linear_gates(const void* a, const void* beta_in, const float* A_log,
+                                           const float* dt_bias, void* g_out, void* beta_out,
+                                           int heads, hipStream_t stream) {
+  qh_launch_linear_gates(a, beta_in, A_log, dt_bias, (float*)g_out, beta_out, heads, stream);
+  check_launch("launch_prepare_linear_gates");
+}
+
+QH_EXPORT void launch_rmsnorm_gated_decode(const void* core, const void* z, const void* weight,
+                                           void* out, int heads, int head_dim, float eps,
+                                           hipStream_t stream) {
+  if (head_dim <= 0 || head_dim > 256) {
+    qh_set_error("launch_rmsnorm_gated_decode: head_dim=%d unsupported (<= 256)", head_dim);
+    return;
+  }
+  qh_launch_gated_rmsnorm(core, z, weight, out, heads, head_dim, eps, 0, stream);
+  check_launch("launch_rmsnorm_gated_decode");
+}
+
+QH_EXPORT void launch_delta_rule_decode(const void* q, const void* k, const void* v, const void* g,
+                                        const void* beta, void* state, void* output, int n_heads,
+                                        int head_dim, hipStream_t stream) {
+  if (qh_launch_delta_rule(q, k, v, (const float*)g, beta, (float*)state, output, n_heads,
+                           head_dim, stream) == 0)
+    check_launch("launch_delta_rule_decode");
+}
+
+QH_EXPORT void fp8_gemm_batch(const void* x_bf16, const void* w_fp8, const void* w_scale_bf16,
+                              void* y_bf16, int M, int N, int K, int K_blocks,
+                              hipStream_t stream) {
+  if (M <= 0) return;
+  if (!k_ok(K, "fp8_gemm_batch")) return;
+  if (qh_launch_gemm_e4m3(x_bf16, w_fp8, w_scale_bf16, y_bf16, M, N, K, K_blocks, true, stream) == 0)
+    check_launch("fp8_gemm_batch");
+}
+
+// ============================================================================
+// Native entry points (fp32 scale_inv)
+// ============================================================================
+// Grouped block-scaled GEMV sharing one activation vector (up to 4 segments).
+QH_EXPORT int qh_gemv_e4m3(const void* x, const void* x2, const float* norm_w, float eps, int K,
+                           const void* res1, const void* res2, int nseg, const void* w0,
+                           const void* s0, void* y0, int n0, int kb0, const void* w1,
+                           const void* s1, void* y1, int n1, int kb1, const void* w2,
+                           const void* s2, void* y2, int n2, int kb2, const void* w3,
+                           const void* s3, void* y3, int n3, int kb3, int scales_bf16,
+                           hipStream_t stream) {
+  if (nseg < 1 || nseg > 4) {
+    qh_set_error("qh_gemv_e4m3: nseg=%d must be 1..4", nseg);
+    return -1;
+  }
+  QhGemvParams p = gemv_params(x, K);
+  p.x2 = (const uint16_t*)x2;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.res1 = (const uint16_t*)res1;
+  p.res2 = (const uint16_t*)res2;
+  p.nseg = nseg;
+  p.seg[0] = seg(w0, s0, y0, n0, kb0);
+  p.seg[1] = seg(w1, s1, y1, n1, kb1);
+  p.seg[2] = seg(w2, s2, y2, n2, kb2);
+  p.seg[3] = seg(w3, s3, y3, n3, kb3);
+  if ((res1 || res2) && nseg != 1) {
+    qh_set_error("qh_gemv_e4m3: residual epilogue needs a single segment");
+    return -1;
+  }
+  return run_gemv(p, scales_bf16 != 0, "qh_gemv_e4m3", stream);
+}
+
+// Paired gate/up GEMV with (1+w) RMSNorm prologue and SiLU(gate)*up epilogue.
+QH_EXPORT int qh_mlp_gate_up(const void* x, const void* x2, const float* norm_w, float eps, int K,
+                             const void* w_g, const void* s_g, const void* w_u, const void* s_u,
+                             int N, int kb, void* m_out, void* g_out, void* u_out,
+                             int scales_bf16, hipStream_t stream) {
+  if (!k_ok(K, "qh_mlp_gate_up")) return -1;
+  QhMlpParams m;
+  memset(&m, 0, sizeof(m));
+  m.x = (const uint16_t*)x;
+  m.x2 = (const uint16_t*)x2;
+  m.norm_w = norm_w;
+  m.eps = eps;
+  m.K = K;
+  m.wg = (const uint8_t*)w_g;
+  m.sg = s_g;
+  m.wu = (const uint8_t*)w_u;
+  m.su = s_u;
+  m.N = N;
+  m.kb = kb;
+  m.m_out = (uint16_t*)m_out;
+  m.g_out = (uint16_t*)g_out;
+  m.u_out = (uint16_t*)u_out;
+  if (qh_launch_mlp(m, scales_bf16 != 0, stream) != 0) return -1;
+  return check_launch("qh_mlp_gate_up");
+}
+
+// Whole decode MLP: h2 = bf16(h + o) (o optional), m = silu(g)*u of
+// RMSNorm(h2), out = bf16(h2 + bf16(W_d m)).
+QH_EXPORT int qh_mlp_decode(const void* h, const void* o, const float* norm_w, float eps, int H,
+                            const void* w_g, const void* s_g, const void* w_u, const void* s_u,
+                            int I, int kb_gu, const void* w_d, const void* s_d, int kb_d,
+                            void* m_buf, void* out, int scales_bf16, hipStream_t stream) {
+  if (qh_mlp_gate_up(h, o, norm_w, eps, H, w_g, s_g, w_u, s_u, I, kb_gu, m_buf, nullptr, nullptr,
+                     scales_bf16, stream) != 0)
+    return -1;
+  return qh_gemv_e4m3(m_buf, nullptr, nullptr, eps, I, h, o, 1, w_d, s_d, out, H, kb_d, nullptr,
+                      nullptr, nullptr, 0, 0, nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr,
+                      nullptr, 0, 0, scales_bf16, stream);
+}
+
+QH_EXPORT int qh_rmsnorm(const void* x, const float* w, void* out, int rows, int D, float eps,
+                         hipStream_t stream) {
+  if (rows < 0 || D <= 0) {
+    qh_set_error("qh_rmsnorm: bad shape rows=%d D=%d", rows, D);
+    return -1;
+  }
+  qh_launch_rmsnorm_rows(x, w, out, rows, D, eps, stream);
+  return check_launch("qh_rmsnorm");
+}
+
+QH_EXPORT size_t qh_attn_scratch_bytes(int n_kv_heads, int nsplit, int head_dim) {
+  return qh_attn_scratch_floats(n_kv_heads, nsplit, head_dim) * sizeof(float);
+}
+
+// Full-attention decode: q/k head norm, partial RoPE, KV-cache write, split-K
+// GQA attention and the optional sigmoid output gate.  pos_dev (device int) or
+// the host pos gives the token position t: RoPE at t, cache slot t, t+1 keys.
+QH_EXPORT int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_stride,
+                             const void* k_new, const void* v_new, const float* q_norm_w,
+                             const float* k_norm_w, const float* cos_t, const float* sin_t,
+                             void* k_cache, void* v_cache, int max_seq, int head_dim, int rot,
+                             int n_heads, int n_kv, const int* pos_dev, int pos, int nsplit,
+                             void* scratch, unsigned* counters, void* out, float eps,
+                             hipStream_t stream) {
+  QhAttnParams a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q;
+  a.q_stride = q_stride;
+  a.gate = (const uint16_t*)gate;
+  a.gate_stride = gate_stride;
+  a.k_new = (const uint16_t*)k_new;
+  a.v_new = (const uint16_t*)v_new;
+  a.q_norm_w = q_norm_w;
+  a.k_norm_w = k_norm_w;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.k_cache = (uint16_t*)k_cache;
+  a.v_cache = (uint16_t*)v_cache;
+  a.max_seq = max_seq;
+  a.rot = rot;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.pos_dev = pos_dev;
+  a.rope_pos = pos;
+  a.slot = pos;
+  a.total = pos + 1;
+  a.nsplit = nsplit;
+  a.part = (float*)scratch;
+  a.counters = counters;
+  a.out = (uint16_t*)out;
+  a.eps = eps;
+  if (qh_launch_attn(a, head_dim, stream) != 0) return -1;
+  return check_launch("qh_attn_decode");
+}
+
+QH_EXPORT int qh_gdn_decode(const void* mixed, const void* a, const void* b, const void* z,
+                            void* conv_ring, const void* conv_w, const float* A_log,
+                            const float* dt_bias, const void* norm_w, float* state, void* core,
+                            void* out, unsigned* counters, const int* pos_dev, int pos, int Hk,
+                            int Hv, int dk, int dv, float eps, hipStream_t stream) {
+  QhGdnParams g;
+  memset(&g, 0, sizeof(g));
+  g.mixed = (const uint16_t*)mixed;
+  g.a = (const uint16_t*)a;
+  g.b = (const uint16_t*)b;
+  g.z = (const uint16_t*)z;
+  g.conv_ring = (uint16_t*)conv_ring;
+  g.conv_w = (const uint16_t*)conv_w;
+  g.A_log = A_log;
+  g.dt_bias = dt_bias;
+  g.norm_w = (const uint16_t*)norm_w;
+  g.state = state;
+  g.core = (uint16_t*)core;
+  g.out = (uint16_t*)out;
+  g.counters = counters;
+  g.pos_dev = pos_dev;
+  g.pos = pos;
+  g.Hk = Hk;
+  g.Hv = Hv;
+  g.dk = dk;
+  g.dv = dv;
+  g.eps = eps;
+  if (qh_launch_gdn_decode(g, stream) != 0) return -1;
+  return check_launch("qh_gdn_decode");
+}
+
+QH_EXPORT size_t qh_lm_head_scratch_bytes(int N) {
+  return (size_t)qh_lm_head_grid(N) * (sizeof(float) + sizeof(int));
+}
+
+// bf16 lm_head GEMV with fused final (1+w) RMSNorm and greedy argmax.  The
+// last block writes the token (int64) to tok_out; with pos_dev it also stores
+// it at tok_hist[*pos_dev] (when in range) and increments *pos_dev; with embed
+// it copies embed[token] into embed_out for the next step.
+QH_EXPORT int qh_lm_head_argmax(const void* x, const float* norm_w, float eps, int K,
+                                const void* w, int N, void* logits, void* scratch,
+                                unsigned* counter, int64_t* tok_out, int64_t* tok_hist,
+                                int hist_len, int* pos_dev, const void* embed, void* embed_out,
+                                hipStream_t stream) {
+  if (!k_ok(K, "qh_lm_head_argmax")) return -1;
+  if (N <= 0 || !scratch || !counter || !tok_out) {
+    qh_set_error("qh_lm_head_argmax: N=%d, scratch/counter/tok_out required", N);
+    return -1;
+  }
+  QhLmHeadParams p;
+  memset(&p, 0, sizeof(p));
+  const int grid = qh_lm_head_grid(N);
+  p.x = (const uint16_t*)x;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.K = K;
+  p.w = (const uint16_t*)w;
+  p.N = N;
+  p.logits = (uint16_t*)logits;
+  p.part_val = (float*)scratch;
+  p.part_idx = (int*)((float*)scratch + grid);
+  p.counter = counter;
+  p.tok_out = tok_out;
+  p.tok_hist = tok_hist;
+  p.hist_len = hist_len;
+  p.pos = pos_dev;
+  p.embed = (const uint16_t*)embed;
+  p.embed_out = (uint16_t*)embed_out;
+  if (qh_launch_lm_head(p, grid, stream) != 0) return -1;
+  return check_launch("qh_lm_head_argmax");
+}
+
+QH_EXPORT int qh_embed(const void* table, const int64_t* ids, void* out, int n, int K, int vocab,
+                       hipStream_t stream) {
+  qh_launch_embed_gather(table, ids, out, n, K, vocab, stream);
+  return check_launch("qh_embed");
+}
+
+QH_EXPORT int qh_add_bf16(const void* a, const void* b, void* out, int n, hipStream_t stream) {
+  qh_launch_add_bf16(a, b, out, n, stream);
+  return check_launch("qh_add_bf16");
+}
+
+QH_EXPORT int qh_linear_gates(const void* a, const void* b, const float* A_log,
+                              const float* dt_bias, float* g_out, void* beta_out, int heads,
+                              hipStream_t stream) {
+  qh_launch_linear_gates(a, b, A_log, dt_bias, g_out, beta_out, heads, stream);
+  return check_launch("qh_linear_gates");
+}
+
+QH_EXPORT int qh_gated_rmsnorm(const void* core, const void* z, const void* w, void* out,
+                               int heads, int head_dim, float eps, int bf16_steps,
+                               hipStream_t stream) {
+  if (head_dim <= 0 || head_dim > 256) {
+    qh_set_error("qh_gated_rmsnorm: head_dim=%d unsupported (<= 256)", head_dim);
+    return -1;
+  }
+  qh_launch_gated_rmsnorm(core, z, w, out, heads, head_dim, eps, bf16_steps, stream);
+  return check_launch("qh_gated_rmsnorm");
+}
+
+QH_EXPORT size_t qh_gemm_workspace_size(int M, int K) { return qh_gemm_workspace_bytes(M, K); }
+
+// Prefill block-scaled E4M3 GEMM: Y[M,N] = bf16(X[M,K] . deq(W)[N,K]^T) on the
+// fp8 matrix cores.  `ws` (qh_gemm_workspace_size bytes) holds the split
+// activations; when null the library uses an internal buffer.
+QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N,
+                           int K, int kb, int scales_bf16, void* ws, hipStream_t stream) {
+  if (!k_ok(K, "qh_gemm_e4m3")) return -1;
+  if (M <= 0 || N <= 0) return 0;
+  const int rc = ws ? qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scales_bf16 != 0, ws, stream)
+                    : qh_launch_gemm_e4m3(x, w, s, y, M, N, K, kb, scales_bf16 != 0, stream);
+  if (rc != 0) return -1;
+  return check_launch("qh_gemm_e4m3");
+}

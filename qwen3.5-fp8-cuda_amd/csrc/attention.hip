@@ -1,0 +1,344 @@
+// Batch-1 GQA decode attention for the full-attention layers (gfx950).
+//
+// Semantics (reference: qwen3_infer/csrc/fused_kernels.cu:1224-1297
+// layer_mid_attn, 787-867 fused_attn_v2_kernel, 872-903 rope_decode_kernel,
+// 1199-1219 kv_cache_write_kernel; gate: main.py:1059):
+//   q_h  = bf16 RMSNorm_(1+w)(q_h)           (per head, D dims, eps 1e-6)
+//   k    = bf16 RMSNorm_(1+w)(k)
+//   q,k  = bf16 partial RoPE on dims [0, rot): pairs (c, c + rot/2),
+//          out0 = x0 cos - x1 sin, out1 = x1 cos + x0 sin  at position `pos`
+//   K/V cache[kv, slot] = k, v
+//   o_h  = softmax(q_h . K[kv(h)]^T / sqrt(D)) V[kv(h)] over `total` positions,
+//          kv(h) = h * n_kv / n_heads, fp32 softmax, bf16 output
+//   optional gate: out_h = bf16(o_h) * bf16(sigmoid(gate_h))
+//
+// Design: one workgroup per (kv head, position split).  The 4 waves share one
+// K/V tile (32 positions) staged in LDS, each wave serving one query head of
+// the GQA group, so each KV head is read from HBM exactly once per step.  Each
+// split keeps an online-softmax state; the last split to finish for a KV head
+// (atomic arrival counter, self-resetting) merges the partial states and
+// applies the output gate.  The new token's K/V come from registers, so no
+// split ever waits on another.
+#include "qh_common.h"
+#include "qh_attn.h"
+
+namespace {
+
+constexpr int TP = 32;  // positions per LDS tile
+constexpr int MAXG = 8;  // query heads per KV head supported
+
+template <int NPL>
+__device__ __forceinline__ void load_head(float (&v)[NPL], const uint16_t* src) {
+  if constexpr (NPL == 4) {
+    const u32x2 u = *(const u32x2*)src;
+    v[0] = bf_lo(u.x); v[1] = bf_hi(u.x); v[2] = bf_lo(u.y); v[3] = bf_hi(u.y);
+  } else {
+    const uint32_t u = *(const uint32_t*)src;
+    v[0] = bf_lo(u); v[1] = bf_hi(u);
+  }
+}
+
+template <int NPL>
+__device__ __forceinline__ void store_head(uint16_t* dst, const float (&v)[NPL]) {
+  if constexpr (NPL == 4) {
+    *(u32x2*)dst = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+  } else {
+    *(uint32_t*)dst = pack_bf2(v[0], v[1]);
+  }
+}
+
+// bf16 (1+w) RMSNorm over a D-wide head held NPL values per lane, then bf16
+// partial RoPE.  All lanes of the wave must call this.
+template <int D>
+__device__ __forceinline__ void norm_rope(float (&v)[D / 64], const float* norm_w, float eps,
+                                          const float* cos_row, const float* sin_row, int rot,
+                                          int lane) {
+  constexpr int NPL = D / 64;
+  if (norm_w) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) ss = fmaf(v[i], v[i], ss);
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) v[i] = rbf(v[i] * r * (1.0f + norm_w[lane * NPL + i]));
+  }
+  if (rot > 0) {
+    const int half = rot >> 1;
+    const int pm = half / NPL;  // partner lane distance (power of two, checked on the host)
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const float partner = __shfl_xor(v[i], pm, 64);
+      const int c = lane * NPL + i;
+      if (c < half) {
+        v[i] = rbf(v[i] * cos_row[c] - partner * sin_row[c]);
+      } else if (c < rot) {
+        v[i] = rbf(v[i] * cos_row[c] + partner * sin_row[c]);
+      }
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
+  constexpr int NPL = D / 64;
+  constexpr int KS = D + 16;  // padded K row (bf16): conflict-free 16-byte LDS reads
+  constexpr int HPW = MAXG / 4;
+  __shared__ __align__(16) uint16_t sK[TP * KS];
+  __shared__ __align__(16) uint16_t sV[TP * D];
+  __shared__ __align__(16) uint16_t sQ[MAXG * D];
+  __shared__ float sP[MAXG][TP];
+  __shared__ __align__(16) uint16_t sKn[D];
+  __shared__ __align__(16) uint16_t sVn[D];
+  __shared__ int s_last;
+
+  const int kvh = blockIdx.x;
+  const int split = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
+  const int G = p.n_heads / p.n_kv;
+
+  int rope_pos = p.rope_pos, slot = p.slot, total = p.total;
+  if (p.pos_dev) {
+    const int t = *p.pos_dev;
+    rope_pos = t;
+    slot = t;
+    total = t + 1;
+  }
+  // A device-resident position past the cache touches nothing (bounds guard).
+  if (slot < 0 || slot >= p.max_seq || total > p.max_seq) return;
+  int span = (total + p.nsplit - 1) / p.nsplit;
+  span = ((span + TP - 1) / TP) * TP;
+  const int p0 = split * span;
+  const int p1 = min(total, p0 + span);
+  const bool slot_in_range = slot >= 0 && slot < total;
+  const bool owner = (slot >= p0 && slot < p1) || (split == 0 && !slot_in_range);
+  const float* cos_row = p.cos_t + (size_t)rope_pos * p.rot;
+  const float* sin_row = p.sin_t + (size_t)rope_pos * p.rot;
+  const float scale = rsqrtf((float)D);
+
+  // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
+  for (int gi = wid; gi < G; gi += 4) {
+    const int h = kvh * G + gi;
+    float qv[NPL];
+    load_head<NPL>(qv, p.q + (size_t)h * p.q_stride + lane * NPL);
+    norm_rope<D>(qv, p.q_norm_w, p.eps, cos_row, sin_row, p.rot, lane);
+    store_head<NPL>(sQ + gi * D + lane * NPL, qv);
+    if (p.q_wb && split == 0) store_head<NPL>(p.q_wb + (size_t)h * D + lane * NPL, qv);
+  }
+  // ---- the new token's K (norm + RoPE) and V -------------------------------
+  if (wid == 0 && p.k_new) {
+    float kv[NPL], vv[NPL];
+    load_head<NPL>(kv, p.k_new + (size_t)kvh * D + lane * NPL);
+    load_head<NPL>(vv, p.v_new + (size_t)kvh * D + lane * NPL);
+    norm_rope<D>(kv, p.k_norm_w, p.eps, cos_row, sin_row, p.rot, lane);
+    store_head<NPL>(sKn + lane * NPL, kv);
+    store_head<NPL>(sVn + lane * NPL, vv);
+    if (owner) {
+      const size_t off = ((size_t)kvh * p.max_seq + slot) * D + lane * NPL;
+      store_head<NPL>(p.k_cache + off, kv);
+      store_head<NPL>(p.v_cache + off, vv);
+      if (p.k_wb) store_head<NPL>(p.k_wb + (size_t)kvh * D + lane * NPL, kv);
+    }
+  }
+  __syncthreads();
+
+  float m[HPW], l[HPW], o[HPW][NPL];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    m[hi] = -INFINITY;
+    l[hi] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) o[hi][i] = 0.0f;
+  }
+  const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
+  const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
+  const bool new_kv = p.k_new != nullptr;
+
+  for (int t0 = p0; t0 < p1; t0 += TP) {
+    for (int idx = threadIdx.x; idx < TP * (D / 8); idx += 256) {
+      const int row = idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const int pos = t0 + row;
+      u32x4 kq = {0u, 0u, 0u, 0u}, vq = {0u, 0u, 0u, 0u};
+      if (pos < p1) {
+        if (new_kv && pos == slot) {
+          kq = *(const u32x4*)(sKn + c8);
+          vq = *(const u32x4*)(sVn + c8);
+        } else {
+          kq = *(const u32x4*)(kbase + (size_t)pos * D + c8);
+          vq = *(const u32x4*)(vbase + (size_t)pos * D + c8);
+        }
+      }
+      *(u32x4*)(sK + row * KS + c8) = kq;
+      *(u32x4*)(sV + row * D + c8) = vq;
+    }
+    __syncthreads();
+
+    // scores: lane pair (2j, 2j+1) owns position t0+j, each lane half the dims
+    const int prow = lane >> 1, half = lane & 1;
+    const bool valid = t0 + prow < p1;
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+      const int gi = wid + 4 * hi;
+      if (gi < G) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int c = half; c < D / 8; c += 2) {
+          const u32x4 k8 = *(const u32x4*)(sK + prow * KS + c * 8);
+          const u32x4 q8 = *(const u32x4*)(sQ + gi * D + c * 8);
+          dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.x), as_bf2(k8.x), dot, false);
+          dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.y), as_bf2(k8.y), dot, false);
+          dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.z), as_bf2(k8.z), dot, false);
+          dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.w), as_bf2(k8.w), dot, false);
+        }
+        dot += __shfl_xor(dot, 1, 64);
+        const float s = valid ? dot * scale : -INFINITY;
+        const float tmax = wave_max(s);
+        const float nm = fmaxf(m[hi], tmax);
+        const float corr = __expf(m[hi] - nm);
+        const float pv = valid ? __expf(s - nm) : 0.0f;
+        const float psum = wave_sum(half == 0 ? pv : 0.0f);
+        l[hi] = l[hi] * corr + psum;
+        m[hi] = nm;
+        if (half == 0) sP[gi][prow] = pv;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) o[hi][i] *= corr;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+      const int gi = wid + 4 * hi;
+      if (gi < G) {
+#pragma unroll 8
+        for (int j = 0; j < TP; ++j) {
+          const float pj = sP[gi][j];
+          float vv[NPL];
+          load_head<NPL>(vv, sV + j * D + lane * NPL);
+#pragma unroll
+          for (int i = 0; i < NPL; ++i) o[hi][i] = fmaf(pj, vv[i], o[hi][i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  auto emit = [&](int gi, float (&ov)[NPL], float inv) {
+    const int h = kvh * G + gi;
+    float r[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      float a = ov[i] * inv;
+      if (p.gate) {
+        const float gv = bf2f(p.gate[(size_t)h * p.gate_stride + lane * NPL + i]);
+        a = rbf(a) * rbf(qh_sigmoid(gv));
+      }
+      r[i] = a;
+    }
+    store_head<NPL>(p.out + (size_t)h * D + lane * NPL, r);
+  };
+
+  if (p.nsplit == 1) {
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+      const int gi = wid + 4 * hi;
+      if (gi < G) emit(gi, o[hi], 1.0f / l[hi]);
+    }
+    return;
+  }
+
+  // ---- publish this split's partial state; the last split merges ---------
+  const int rec = D + 2;
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi;
+    if (gi < G) {
+      float* dst = p.part + ((size_t)(kvh * p.nsplit + split) * MAXG + gi) * rec;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) dst[lane * NPL + i] = o[hi][i];
+      if (lane == 0) { dst[D] = m[hi]; dst[D + 1] = l[hi]; }
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(p.counters + kvh, 1u);
+    s_last = prev == (unsigned)(p.nsplit - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi;
+    if (gi >= G) continue;
+    float M = -INFINITY;
+    for (int s = 0; s < p.nsplit; ++s) {
+      const float* src = p.part + ((size_t)(kvh * p.nsplit + s) * MAXG + gi) * rec;
+      const float ls = __hip_atomic_load(src + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float ms = __hip_atomic_load(src + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (ls > 0.0f) M = fmaxf(M, ms);
+    }
+    float L = 0.0f, acc[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
+    for (int s = 0; s < p.nsplit; ++s) {
+      const float* src = p.part + ((size_t)(kvh * p.nsplit + s) * MAXG + gi) * rec;
+      const float ls = __hip_atomic_load(src + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (!(ls > 0.0f)) continue;
+      const float ms = __hip_atomic_load(src + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float w = __expf(ms - M);
+      L = fmaf(ls, w, L);
+#pragma unroll
+      for (int i = 0; i < NPL; ++i)
+        acc[i] = fmaf(__hip_atomic_load(src + lane * NPL + i, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT),
+                      w, acc[i]);
+    }
+    emit(gi, acc, 1.0f / L);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+size_t qh_attn_scratch_floats(int n_kv, int nsplit, int head_dim) {
+  return (size_t)n_kv * nsplit * MAXG * (head_dim + 2);
+}
+
+int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
+  if (p.n_kv <= 0 || p.n_heads % p.n_kv != 0 || p.n_heads / p.n_kv > MAXG) {
+    qh_set_error("attn: n_heads=%d n_kv_heads=%d unsupported (group size must divide and be <= %d)",
+                 p.n_heads, p.n_kv, MAXG);
+    return -1;
+  }
+  if (head_dim != 128 && head_dim != 256) {
+    qh_set_error("attn: head_dim=%d unsupported (128 or 256)", head_dim);
+    return -1;
+  }
+  const int npl = head_dim / 64;
+  if (p.rot < 0 || p.rot > head_dim || (p.rot % 2) != 0 ||
+      (p.rot > 0 && (((p.rot / 2) % npl) != 0 || ((p.rot / 2 / npl) & (p.rot / 2 / npl - 1)) != 0))) {
+    qh_set_error("attn: rotary_dim=%d unsupported for head_dim=%d", p.rot, head_dim);
+    return -1;
+  }
+  if (p.nsplit < 1 || (p.nsplit > 1 && (!p.part || !p.counters))) {
+    qh_set_error("attn: split-K needs scratch and counters");
+    return -1;
+  }
+  if (!p.pos_dev) {
+    if (p.total < 1 || p.total > p.max_seq || p.slot < 0 || p.slot >= p.max_seq || p.rope_pos < 0) {
+      qh_set_error("attn: positions out of range (pos=%d slot=%d total=%d max_seq=%d)", p.rope_pos,
+                   p.slot, p.total, p.max_seq);
+      return -1;
+    }
+  }
+  dim3 grid(p.n_kv, p.nsplit);
+  if (head_dim == 256)
+    hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, p);
+  return 0;
+}

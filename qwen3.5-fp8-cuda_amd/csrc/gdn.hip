@@ -1,0 +1,252 @@
+// GatedDeltaNet ("linear attention") single-token decode step on gfx950.
+//
+// Semantics (reference: main.py:1064-1162 linear_attention_forward with s == 1,
+// main.py:1165-1199 delta rule, qwen3_infer/csrc/fused_kernels.cu:623-684
+// delta_rule_decode_kernel; conv update = transformers causal_conv1d_update,
+// modeling_qwen3_5.py:200-217):
+//   conv   : y_c = bf16(silu(bf16(sum_i w[c,i] * x_{t-3+i})))  (window of 4)
+//   gates  : beta = bf16(sigmoid(b)), g = -exp(A_log) * softplus(a + dt_bias)
+//   per value head h (key head h / (Hv/Hk)):
+//     q^ = q / sqrt(sum q^2 + 1e-6) / sqrt(dk),  k^ = k / sqrt(sum k^2 + 1e-6)  (fp32)
+//     S  <- S * e^g;  d = (v - S^T k^) * beta;  S <- S + k^ d^T;  o = S^T q^
+//   core = bf16(o); out = bf16(bf16(bf16(core * rsqrt(mean core^2 + eps)) * w)
+//                              * bf16(silu(z)))   (main.py:1152-1158)
+//
+// Design: the fp32 state S[h] (dk x dv) is split by value columns; one
+// 256-thread workgroup owns 32 columns of one head (8 row groups x 32
+// columns), so a step reads and writes every state byte exactly once, spread
+// over Hv * dv / 32 workgroups.  Each workgroup recomputes the conv + l2norm of
+// its key head's q/k (256 channels, cheap) so workgroups never wait on each
+// other.  The conv state is a 4-slot ring indexed by position (slot t % 4
+// holds x_t): readers of slots t-1..t-3 and the writer of slot t never
+// collide.  The gated RMSNorm needs a whole head: the last of a head's column
+// workgroups to finish (self-resetting arrival counter) applies it.
+#include "qh_common.h"
+#include "qh_gdn.h"
+
+namespace {
+
+constexpr int VS = 32;  // value columns per workgroup
+
+// Delta-rule update of 32 value columns.  Thread t: column t & 31, rows
+// (t >> 5) * DK/8 .. +DK/8.  qn/kn: normalised q, k (fp32, LDS).
+template <int DK>
+__device__ __forceinline__ float delta_columns(float* state_cols, int dv, const float* qn,
+                                               const float* kn, float vval, float beta,
+                                               float decay, float* red) {
+  constexpr int RPT = DK / 8;
+  const int j = threadIdx.x & 31;
+  const int rg = threadIdx.x >> 5;
+  float S[RPT];
+  float pred = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    S[r] = state_cols[(size_t)(rg * RPT + r) * dv + j];
+    pred = fmaf(S[r] * decay, kn[rg * RPT + r], pred);
+  }
+  red[rg * 32 + j] = pred;
+  __syncthreads();
+  pred = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) pred += red[g * 32 + j];
+  const float delta = (vval - pred) * beta;
+  float o = 0.0f;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const float upd = fmaf(kn[rg * RPT + r], delta, S[r] * decay);
+    state_cols[(size_t)(rg * RPT + r) * dv + j] = upd;
+    o = fmaf(upd, qn[rg * RPT + r], o);
+  }
+  __syncthreads();
+  red[rg * 32 + j] = o;
+  __syncthreads();
+  o = 0.0f;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) o += red[g * 32 + j];
+  return o;
+}
+
+// Sum over the 128 threads [base, base+128) of a 256-thread block.
+__device__ __forceinline__ float half_block_sum(float v, float* red2) {
+  v = wave_sum(v);
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red2[wid] = v;
+  __syncthreads();
+  const int base = (wid >> 1) * 2;
+  return red2[base] + red2[base + 1];
+}
+
+template <int DK>
+__global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
+  static_assert(DK == 128, "fused decode step assumes dk = 128");
+  __shared__ float qn[DK], kn[DK];
+  __shared__ float red[8 * 32];
+  __shared__ float red2[4];
+  __shared__ float vconv[VS];
+  __shared__ int s_last;
+
+  const int h = blockIdx.x;
+  const int sidx = blockIdx.y;
+  const int r = p.Hv / p.Hk;
+  const int kh = h / r;
+  const int t = p.pos_dev ? *p.pos_dev : p.pos;
+  const int dv = p.dv;
+  const int tid = threadIdx.x;
+
+  // ---- causal conv (window of 4) + SiLU for q/k of key head kh ------------
+  {
+    const int i = tid & (DK - 1);
+    const bool is_k = tid >= DK;
+    const int c = (is_k ? p.Hk * DK : 0) + kh * DK + i;
+    const uint16_t x_t = p.mixed[c];
+    const uint16_t* ring = p.conv_ring + (size_t)c * 4;
+    const uint16_t* w = p.conv_w + (size_t)c * 4;
+    float acc = bf2f(w[3]) * bf2f(x_t);
+    acc = fmaf(bf2f(w[2]), bf2f(ring[(t + 3) & 3]), acc);
+    acc = fmaf(bf2f(w[1]), bf2f(ring[(t + 2) & 3]), acc);
+    acc = fmaf(bf2f(w[0]), bf2f(ring[(t + 1) & 3]), acc);
+    const float y = rbf(qh_silu(rbf(acc)));
+    if (sidx == 0 && (h % r) == 0) p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
+    const float ss = half_block_sum(y * y, red2);
+    if (is_k) kn[i] = y * rsqrtf(ss + 1e-6f);
+    else qn[i] = y * rsqrtf(ss + 1e-6f) * rsqrtf((float)DK);
+  }
+  if (tid < VS) {
+    const int c = 2 * p.Hk * DK + h * dv + sidx * VS + tid;
+    const uint16_t x_t = p.mixed[c];
+    const uint16_t* ring = p.conv_ring + (size_t)c * 4;
+    const uint16_t* w = p.conv_w + (size_t)c * 4;
+    float acc = bf2f(w[3]) * bf2f(x_t);
+    acc = fmaf(bf2f(w[2]), bf2f(ring[(t + 3) & 3]), acc);
+    acc = fmaf(bf2f(w[1]), bf2f(ring[(t + 2) & 3]), acc);
+    acc = fmaf(bf2f(w[0]), bf2f(ring[(t + 1) & 3]), acc);
+    vconv[tid] = rbf(qh_silu(rbf(acc)));
+    p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
+  }
+  // ---- gates ----------------------------------------------------------------
+  const float beta = rbf(qh_sigmoid(bf2f(p.b[h])));
+  const float g = -__expf(p.A_log[h]) * qh_softplus(bf2f(p.a[h]) + p.dt_bias[h]);
+  const float decay = __expf(g);
+  __syncthreads();
+
+  float* cols = p.state + (size_t)h * DK * dv + sidx * VS;
+  const float o = delta_columns<DK>(cols, dv, qn, kn, vconv[tid & 31], beta, decay, red);
+  const int j = tid & 31;
+  if (tid < 32) p.core[(size_t)h * dv + sidx * VS + j] = f2bf(o);
+
+  // ---- gated RMSNorm by the last column workgroup of this head ------------
+  const int nslice = dv / VS;
+  if (nslice > 1) {
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned prev = atomicAdd(p.counters + h, 1u);
+      s_last = prev == (unsigned)(nslice - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+  } else {
+    __syncthreads();
+  }
+  // dv <= 256: one element per thread
+  const bool ok = tid < dv;
+  float x = 0.0f;
+  if (ok) {
+    const uint16_t* src = p.core + (size_t)h * dv + tid;
+    const uint32_t word = __hip_atomic_load((const uint32_t*)((uintptr_t)src & ~(uintptr_t)3),
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    x = (tid & 1) ? bf_hi(word) : bf_lo(word);
+  }
+  float ss = wave_sum(x * x);
+  __syncthreads();
+  if ((tid & 63) == 0) red2[tid >> 6] = ss;
+  __syncthreads();
+  ss = red2[0] + red2[1] + red2[2] + red2[3];
+  if (ok) {
+    const float rs = rsqrtf(ss / (float)dv + p.eps);
+    const float normed = rbf(rbf(x * rs) * bf2f(p.norm_w[tid]));
+    const float sz = rbf(qh_silu(bf2f(p.z[(size_t)h * dv + tid])));
+    p.out[(size_t)h * dv + tid] = f2bf(normed * sz);
+  }
+  if (nslice > 1 && tid == 0)
+    __hip_atomic_store(p.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reference ABI delta rule (fused_kernels.cu:623-684): q, k already expanded to
+// one row per value head, g fp32, beta bf16, state updated in place, bf16 out.
+template <int DK>
+__global__ __launch_bounds__(256) void delta_rule_kernel(const uint16_t* q, const uint16_t* k,
+                                                         const uint16_t* v, const float* g,
+                                                         const uint16_t* beta, float* state,
+                                                         uint16_t* out) {
+  __shared__ float qn[DK], kn[DK];
+  __shared__ float red[8 * 32];
+  __shared__ float red2[4];
+  const int h = blockIdx.x;
+  const int sidx = blockIdx.y;
+  const int tid = threadIdx.x;
+  // l2norm of q and k: threads [0,128) and [128,256) each own up to DK/128 values
+  {
+    constexpr int PER = DK > 128 ? DK / 128 : 1;
+    const bool is_k = tid >= 128;
+    const int i0 = (tid & 127) * PER;
+    const uint16_t* src = (is_k ? k : q) + (size_t)h * DK;
+    float vals[PER];
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      vals[e] = (i0 + e < DK) ? bf2f(src[i0 + e]) : 0.0f;
+      ss = fmaf(vals[e], vals[e], ss);
+    }
+    ss = half_block_sum(ss, red2);
+    const float sc = is_k ? rsqrtf(ss + 1e-6f) : rsqrtf(ss + 1e-6f) * rsqrtf((float)DK);
+#pragma unroll
+    for (int e = 0; e < PER; ++e)
+      if (i0 + e < DK) (is_k ? kn : qn)[i0 + e] = vals[e] * sc;
+  }
+  __syncthreads();
+  const float decay = __expf(g[h]);
+  const float bt = bf2f(beta[h]);
+  const int j = tid & 31;
+  const float vval = bf2f(v[(size_t)h * DK + sidx * VS + j]);
+  float* cols = state + (size_t)h * DK * DK + sidx * VS;
+  const float o = delta_columns<DK>(cols, DK, qn, kn, vval, bt, decay, red);
+  if (tid < 32) out[(size_t)h * DK + sidx * VS + j] = f2bf(o);
+}
+
+}  // namespace
+
+int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st) {
+  if (p.dk != 128 || p.dv % VS != 0 || p.dv > 256 || p.Hk <= 0 || p.Hv % p.Hk != 0) {
+    qh_set_error("gdn: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk=128, dv%%32==0, dv<=256)",
+                 p.dk, p.dv, p.Hk, p.Hv);
+    return -1;
+  }
+  if (p.dv / VS > 1 && !p.counters) {
+    qh_set_error("gdn: counters required");
+    return -1;
+  }
+  hipLaunchKernelGGL(gdn_decode_kernel<128>, dim3(p.Hv, p.dv / VS), dim3(256), 0, st, p);
+  return 0;
+}
+
+int qh_launch_delta_rule(const void* q, const void* k, const void* v, const float* g,
+                         const void* beta, float* state, void* out, int n_heads, int head_dim,
+                         hipStream_t st) {
+  dim3 grid(n_heads, head_dim / VS);
+#define QH_DR(DKV)                                                                             \
+  hipLaunchKernelGGL(delta_rule_kernel<DKV>, grid, dim3(256), 0, st, (const uint16_t*)q,       \
+                     (const uint16_t*)k, (const uint16_t*)v, g, (const uint16_t*)beta, state, \
+                     (uint16_t*)out)
+  switch (head_dim) {
+    case 64: QH_DR(64); break;
+    case 128: QH_DR(128); break;
+    case 256: QH_DR(256); break;
+    default:
+      qh_set_error("delta_rule: head_dim=%d unsupported (64, 128, 256)", head_dim);
+      return -1;
+  }
+#undef QH_DR
+  return 0;
+}

@@ -1,0 +1,130 @@
+// Shared device helpers for the gfx950 (MI355X) decode kernels.
+//
+// Conventions used by every kernel in this library:
+//   * activations are bf16 stored as raw uint16_t bits (round-to-nearest-even
+//     on every float -> bf16 conversion, like torch's .to(torch.bfloat16));
+//   * FP8 weights are OCP E4M3FN bytes (bias 7, no inf, 0x7F/0xFF = NaN,
+//     max 448), which gfx950 converts natively;
+//   * a wavefront is 64 lanes; workgroups are 256 threads (4 waves) unless a
+//     kernel says otherwise.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define QH_WAVE 64
+
+typedef __bf16 qh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float qh_f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 <-> f32 ----------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// Round-to-nearest-even f32 -> bf16 (hardware v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+// Round a float through bf16 and back (models a bf16 tensor materialisation).
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ qh_bf16x2 as_bf2(uint32_t u) {
+  return __builtin_bit_cast(qh_bf16x2, u);
+}
+
+// ---- E4M3FN -> bf16 / f32 --------------------------------------------------
+// Two E4M3 bytes (word 0 = bytes 0,1; word 1 = bytes 2,3) -> two bf16, exact
+// (every E4M3 value is representable in bf16).  Scale 1.0 = plain conversion.
+__device__ __forceinline__ qh_bf16x2 e4m3x2_lo_bf16(uint32_t p) {
+  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p, 1.0f, false);
+}
+__device__ __forceinline__ qh_bf16x2 e4m3x2_hi_bf16(uint32_t p) {
+  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(p, 1.0f, true);
+}
+__device__ __forceinline__ qh_f32x2 e4m3x2_lo_f32(uint32_t p) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8(p, false);
+}
+__device__ __forceinline__ qh_f32x2 e4m3x2_hi_f32(uint32_t p) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8(p, true);
+}
+
+// Dot product of 8 E4M3 weights (two dwords) with 8 bf16 activations (one
+// u32x4), fp32 accumulate via v_dot2_f32_bf16.
+__device__ __forceinline__ float dot8_e4m3_bf16(uint32_t w0, uint32_t w1, u32x4 x, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(e4m3x2_lo_bf16(w0), as_bf2(x.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(e4m3x2_hi_bf16(w0), as_bf2(x.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(e4m3x2_lo_bf16(w1), as_bf2(x.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(e4m3x2_hi_bf16(w1), as_bf2(x.w), acc, false);
+  return acc;
+}
+// Dot product of 8 bf16 weights with 8 bf16 activations.
+__device__ __forceinline__ float dot8_bf16(u32x4 w, u32x4 x, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w.x), as_bf2(x.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w.y), as_bf2(x.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w.z), as_bf2(x.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w.w), as_bf2(x.w), acc, false);
+  return acc;
+}
+
+// ---- reductions -------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, QH_WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QH_WAVE));
+  return v;
+}
+// Sum over aligned groups of `G` lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, QH_WAVE);
+  return v;
+}
+
+// Block-wide sum for a 256-thread block; `red` must hold >= 4 floats of LDS.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// ---- math --------------------------------------------------------------------
+__device__ __forceinline__ float qh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float qh_silu(float x) { return x / (1.0f + __expf(-x)); }
+// torch.nn.functional.softplus(beta=1, threshold=20)
+__device__ __forceinline__ float qh_softplus(float x) {
+  return x > 20.0f ? x : log1pf(__expf(x));
+}
+
+// ---- scale addressing ----------------------------------------------------
+// Scale-mode encoding of the reference ABI (`K_blocks` argument):
+//   kb > 1  : 128x128 block scales, shape [ceil(N/128), kb]
+//   kb == 1 : one scale per output row, shape [N]
+//   kb < 0  : per-row-per-block scales, shape [N, -kb]
+__device__ __forceinline__ int scale_index(int kb_code, int row, int kblk) {
+  if (kb_code > 1) return (row >> 7) * kb_code + kblk;
+  if (kb_code == 1) return row;
+  return row * (-kb_code) + kblk;
+}
+template <typename ScaleT> __device__ __forceinline__ float load_scale(const ScaleT* s, int i);
+template <> __device__ __forceinline__ float load_scale<float>(const float* s, int i) { return s[i]; }
+template <> __device__ __forceinline__ float load_scale<uint16_t>(const uint16_t* s, int i) {
+  return bf2f(s[i]);
+}

@@ -1,0 +1,12 @@
+// Launchers for the prefill E4M3 GEMM (gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+size_t qh_gemm_workspace_bytes(int M, int K);
+int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y, int M, int N,
+                           int K, int kb, bool scale_bf16, void* ws, hipStream_t st);
+int qh_launch_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
+                        int kb, bool scale_bf16, hipStream_t st);
+void qh_set_error(const char* fmt, ...);

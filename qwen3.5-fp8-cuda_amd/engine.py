@@ -1,0 +1,241 @@
+"""Batch-1 FP8 decode engine for Qwen3.5-shaped hybrid models on one MI355X.
+
+Mirrors the reference engine's public surface (main.py:326-1604,
+``QwenEngineFP8Opt``): ``forward(input_ids, past_len, logits_to_keep=1)``
+returns bf16 logits of the last position, ``_reset_cache()`` clears the
+recurrent state, and the generic decode path's numerics are followed.
+
+Per decode step the GPU runs 5 kernels per layer plus one for the head:
+  full attention : qkv GEMV (+input RMSNorm) -> attention (q/k norm, RoPE,
+                   KV write, split-K, gate) -> o_proj GEMV (+residual)
+  GatedDeltaNet  : in_proj GEMV x4 (+input RMSNorm) -> GDN step (conv, gates,
+                   l2norm, delta rule, gated norm) -> out_proj GEMV (+residual)
+  both           : gate/up GEMV (+post-attn RMSNorm, SiLU*up) -> down GEMV
+                   (+residual)
+  head           : lm_head GEMV (+final RMSNorm) -> greedy argmax -> token,
+                   position += 1, next token's embedding row.
+Token, position and hidden state stay on the device, so one step is a
+replayable HIP graph with no host round trip.
+"""
+import math
+
+import torch
+
+from . import abi
+from . import ops
+
+
+def rope_tables(max_pos, rotary_dim, theta):
+    """fp32 cos/sin [max_pos, rotary_dim] of the partial rotary embedding
+    (main.py:513-533: inv_freq denominator is the rotary dim, emb = cat(f, f)),
+    computed in float64 and rounded once."""
+    inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float64) / rotary_dim))
+    pos = torch.arange(max_pos, dtype=torch.float64)
+    f = torch.outer(pos, inv)
+    emb = torch.cat([f, f], dim=-1)
+    return emb.cos().float().contiguous(), emb.sin().float().contiguous()
+
+
+def default_attn_splits(max_seq):
+    return max(1, min(32, max_seq // 128))
+
+
+class Qwen35FP8Engine:
+    def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda"):
+        if not torch.cuda.is_available():
+            raise RuntimeError("Qwen35FP8Engine needs a GPU (there is no CPU fallback)")
+        self.lib = abi.load()
+        self.cfg = cfg = weights.cfg
+        self.w = weights if weights.embed.is_cuda else weights.to(device)
+        self.device = torch.device(device)
+        self.max_seq_len = max_seq_len
+        self.eps = cfg.rms_norm_eps
+        dev = self.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+        self.h = torch.zeros(H, **bf)
+        self.h2 = torch.zeros(H, **bf)
+        self.q_all = torch.zeros(cfg.q_proj_rows, **bf)
+        self.k_new = torch.zeros(cfg.kv_rows, **bf)
+        self.v_new = torch.zeros(cfg.kv_rows, **bf)
+        self.mixed = torch.zeros(cfg.conv_dim, **bf)
+        self.z = torch.zeros(cfg.value_dim, **bf)
+        self.a = torch.zeros(cfg.linear_num_value_heads, **bf)
+        self.b = torch.zeros(cfg.linear_num_value_heads, **bf)
+        self.mix_out = torch.zeros(max(cfg.attn_out_dim, cfg.value_dim), **bf)
+        self.core = torch.zeros(cfg.value_dim, **bf)
+        self.m = torch.zeros(I, **bf)
+        self.logits = torch.zeros(V, **bf)
+        self.tok = torch.zeros(1, 1, dtype=torch.int64, device=dev)
+        self.tok_hist = torch.zeros(max_seq_len, dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.lm_scratch = torch.zeros(int(self.lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8,
+                                      device=dev)
+        self.lm_counter = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.attn_splits = attn_splits or default_attn_splits(max_seq_len)
+        nbytes = int(self.lib.qh_attn_scratch_bytes(cfg.num_key_value_heads, self.attn_splits,
+                                                    cfg.head_dim))
+        self.attn_scratch = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=dev)
+        self.attn_counters = torch.zeros(cfg.num_key_value_heads, dtype=torch.int32, device=dev)
+        self.gdn_counters = torch.zeros(cfg.linear_num_value_heads, dtype=torch.int32, device=dev)
+        cos, sin = rope_tables(max_seq_len, cfg.rotary_dim, cfg.rope_theta)
+        self.rope_cos, self.rope_sin = cos.to(dev), sin.to(dev)
+        self.k_cache, self.v_cache, self.conv_ring, self.state = [], [], [], []
+        for i in range(cfg.num_hidden_layers):
+            if cfg.is_full(i):
+                shape = (cfg.num_key_value_heads, max_seq_len, cfg.head_dim)
+                self.k_cache.append(torch.zeros(shape, **bf))
+                self.v_cache.append(torch.zeros(shape, **bf))
+                self.conv_ring.append(None)
+                self.state.append(None)
+            else:
+                self.k_cache.append(None)
+                self.v_cache.append(None)
+                self.conv_ring.append(torch.zeros(cfg.conv_dim, cfg.linear_conv_kernel_dim, **bf))
+                self.state.append(torch.zeros(cfg.linear_num_value_heads, cfg.linear_key_head_dim,
+                                              cfg.linear_value_head_dim, dtype=torch.float32,
+                                              device=dev))
+        self.graph = None
+        self.prompt_buf = None
+
+    # ------------------------------------------------------------------ state
+    def _reset_cache(self):
+        """Zero GatedDeltaNet conv/recurrent states; position 0 (main.py:851-895).
+        KV-cache contents need no clearing: every readable slot is rewritten."""
+        for r in self.conv_ring:
+            if r is not None:
+                r.zero_()
+        for s in self.state:
+            if s is not None:
+                s.zero_()
+        self.pos.zero_()
+
+    # ------------------------------------------------------------- launches
+    def _gemv(self, x, segs, norm_w=None, res=None):
+        L = self.lib
+        args = []
+        for i in range(4):
+            if i < len(segs):
+                (w, s), y = segs[i]
+                args += [abi.ptr(w), abi.ptr(s), abi.ptr(y), w.shape[0], ops.scale_mode(w, s)]
+            else:
+                args += [None, None, None, 0, 0]
+        abi.check(L.qh_gemv_e4m3(abi.ptr(x), None, abi.ptr(norm_w), self.eps, x.numel(),
+                                 abi.ptr(res), None, len(segs), *args, 0, abi.stream_handle()),
+                  "gemv")
+
+    def _layer(self, i):
+        cfg, L, ly = self.cfg, self.lib, self.w.layers[i]
+        st = abi.stream_handle()
+        if cfg.is_full(i):
+            self._gemv(self.h, [(ly["q_proj"], self.q_all), (ly["k_proj"], self.k_new),
+                                (ly["v_proj"], self.v_new)], norm_w=ly["input_layernorm"])
+            D = cfg.head_dim
+            gate = self.q_all[D:]
+            abi.check(L.qh_attn_decode(
+                abi.ptr(self.q_all), 2 * D, abi.ptr(gate), 2 * D, abi.ptr(self.k_new),
+                abi.ptr(self.v_new), abi.ptr(ly["q_norm"]), abi.ptr(ly["k_norm"]),
+                abi.ptr(self.rope_cos), abi.ptr(self.rope_sin), abi.ptr(self.k_cache[i]),
+                abi.ptr(self.v_cache[i]), self.max_seq_len, D, cfg.rotary_dim,
+                cfg.num_attention_heads, cfg.num_key_value_heads, abi.ptr(self.pos), 0,
+                self.attn_splits, abi.ptr(self.attn_scratch), abi.ptr(self.attn_counters),
+                abi.ptr(self.mix_out), self.eps, st), "attn_decode")
+            self._gemv(self.mix_out[:cfg.attn_out_dim], [(ly["o_proj"], self.h2)], res=self.h)
+        else:
+            self._gemv(self.h, [(ly["in_proj_qkv"], self.mixed), (ly["in_proj_z"], self.z),
+                                (ly["in_proj_a"], self.a), (ly["in_proj_b"], self.b)],
+                       norm_w=ly["input_layernorm"])
+            abi.check(L.qh_gdn_decode(
+                abi.ptr(self.mixed), abi.ptr(self.a), abi.ptr(self.b), abi.ptr(self.z),
+                abi.ptr(self.conv_ring[i]), abi.ptr(ly["conv1d_w"]), abi.ptr(ly["A_log"]),
+                abi.ptr(ly["dt_bias"]), abi.ptr(ly["norm_w"]), abi.ptr(self.state[i]),
+                abi.ptr(self.core), abi.ptr(self.mix_out), abi.ptr(self.gdn_counters),
+                abi.ptr(self.pos), 0, cfg.linear_num_key_heads, cfg.linear_num_value_heads,
+                cfg.linear_key_head_dim, cfg.linear_value_head_dim, self.eps, st), "gdn_decode")
+            self._gemv(self.mix_out[:cfg.value_dim], [(ly["out_proj"], self.h2)], res=self.h)
+        wg, sg = ly["gate_proj"]
+        wu, su = ly["up_proj"]
+        abi.check(L.qh_mlp_gate_up(abi.ptr(self.h2), None, abi.ptr(ly["post_attention_layernorm"]),
+                                   self.eps, cfg.hidden_size, abi.ptr(wg), abi.ptr(sg), abi.ptr(wu),
+                                   abi.ptr(su), wg.shape[0], ops.scale_mode(wg, sg),
+                                   abi.ptr(self.m), None, None, 0, st), "mlp_gate_up")
+        self._gemv(self.m, [(ly["down_proj"], self.h)], res=self.h2)
+
+    def _head(self, next_embed=True):
+        cfg, L = self.cfg, self.lib
+        abi.check(L.qh_lm_head_argmax(
+            abi.ptr(self.h), abi.ptr(self.w.norm_f), self.eps, cfg.hidden_size,
+            abi.ptr(self.w.lm_head), cfg.vocab_size, abi.ptr(self.logits),
+            abi.ptr(self.lm_scratch), abi.ptr(self.lm_counter), abi.ptr(self.tok),
+            abi.ptr(self.tok_hist), self.max_seq_len, abi.ptr(self.pos),
+            abi.ptr(self.w.embed) if next_embed else None,
+            abi.ptr(self.h) if next_embed else None, abi.stream_handle()), "lm_head_argmax")
+
+    def decode_step_launches(self):
+        """Enqueue one decode step on the current stream: h holds the input
+        token's embedding, pos its position; afterwards logits/tok hold the
+        result, h the next token's embedding and pos = pos + 1."""
+        for i in range(self.cfg.num_hidden_layers):
+            self._layer(i)
+        self._head()
+
+    # ------------------------------------------------------------ graphs
+    def capture(self):
+        """Capture one decode step as a HIP graph (replayed by `step`).
+
+        Runs one eager step first (loads every kernel before capture), so the
+        recurrent state is reset afterwards: call before prefill."""
+        self.decode_step_launches()
+        torch.cuda.synchronize()
+        self._reset_cache()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.decode_step_launches()
+        torch.cuda.synchronize()
+        self._reset_cache()
+        self.graph = g
+        return g
+
+    def step(self):
+        """One greedy decode step from the device-resident token/position."""
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.decode_step_launches()
+
+    # ------------------------------------------------------ reference API
+    @torch.inference_mode()
+    def forward(self, input_ids, past_len=0, logits_to_keep=1):
+        """bf16 logits [1, vocab] of the last input position (main.py:1569-1604)."""
+        if isinstance(input_ids, list):
+            input_ids = torch.tensor([input_ids], dtype=torch.long, device=self.device)
+        ids = input_ids.reshape(-1).to(self.device, torch.int64)
+        s = ids.numel()
+        if past_len < 0 or past_len + s > self.max_seq_len:
+            raise ValueError(f"Sequence range [{past_len}, {past_len + s}) exceeds "
+                             f"max_seq_len={self.max_seq_len}")
+        if logits_to_keep != 1:
+            raise ValueError("only logits_to_keep=1 is supported")
+        st = abi.stream_handle()
+        self.pos.fill_(past_len)
+        for t in range(s):
+            abi.check(self.lib.qh_embed(abi.ptr(self.w.embed), abi.ptr(ids[t:t + 1]),
+                                        abi.ptr(self.h), 1, self.cfg.hidden_size,
+                                        self.cfg.vocab_size, st), "embed")
+            self.step()
+        return self.logits.view(1, -1)
+
+    def prefill(self, ids):
+        """Run the prompt; afterwards tok holds the greedy next token, h its
+        embedding and pos = len(ids)."""
+        self.forward(ids, past_len=0)
+
+    def generate(self, n_steps):
+        """n greedy steps from the current device state (no host sync)."""
+        for _ in range(n_steps):
+            self.step()
+
+    def tokens(self, start, stop):
+        """Greedy tokens chosen at positions [start, stop) (device tensor):
+        tokens(t, t+1) is the token predicted after consuming position t."""
+        return self.tok_hist[start:stop]

@@ -1,0 +1,123 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+public header declares, and rejects invalid arguments before touching HIP."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from qwen35_amd import abi, config, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwen35_fp8_hip.h")
+
+# Every symbol the reference's main.py binds (main.py:108-240).
+REFERENCE_SYMBOLS = [
+    "fp8_gemm_batch", "launch_gemv_v4_extern", "launch_linear_in_proj4", "launch_fused_qkv",
+    "launch_fused_gate_up", "launch_rmsnorm_ip", "launch_rmsnorm_out", "launch_fused_attn_v2",
+    "launch_fused_attn", "layer_mid_attn", "layer_pre_attn", "layer_post_attn",
+    "layer_post_o_fp8_mlp", "launch_prepare_linear_gates", "launch_rmsnorm_gated_decode",
+    "launch_delta_rule_decode",
+]
+
+
+def header_symbols():
+    """Function names declared in the public header (comments stripped)."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    decls = re.findall(r"^(?:const\s+)?(?:void|int|size_t|char)\s*\*?\s*(\w+)\s*\(", text, re.M)
+    return sorted(set(decls))
+
+
+def exported(path):
+    lib = ctypes.CDLL(path)
+    return lambda name: hasattr(lib, name)
+
+
+def test_header_declares_every_reference_symbol():
+    decl = header_symbols()
+    for s in REFERENCE_SYMBOLS + ["launch_gemv_v3_extern"]:
+        assert s in decl, s
+
+
+def test_library_exports_every_declared_symbol():
+    has = exported(abi.library_path())
+    missing = [s for s in header_symbols() if not has(s)]
+    assert not missing, missing
+
+
+def test_binding_covers_reference_argtypes():
+    lib = abi.load()
+    for s in REFERENCE_SYMBOLS:
+        assert s in abi.REFERENCE_ARGTYPES
+        assert getattr(lib, s).argtypes == abi.REFERENCE_ARGTYPES[s]
+    # spot-check arities against the reference declarations (main.py)
+    assert len(abi.REFERENCE_ARGTYPES["launch_gemv_v4_extern"]) == 8
+    assert len(abi.REFERENCE_ARGTYPES["layer_mid_attn"]) == 19
+    assert len(abi.REFERENCE_ARGTYPES["layer_post_attn"]) == 30
+    assert len(abi.REFERENCE_ARGTYPES["layer_post_o_fp8_mlp"]) == 21
+    assert len(abi.REFERENCE_ARGTYPES["launch_linear_in_proj4"]) == 23
+
+
+def test_validation_errors_need_no_gpu():
+    lib = abi.load()
+    rc = lib.qh_gemv_e4m3(None, None, None, 1e-6, 2560, None, None, 5, *([None, None, None, 0, 0] * 4),
+                          0, None)
+    assert rc == -1 and "nseg" in abi.last_error()
+    rc = lib.qh_gemv_e4m3(None, None, None, 1e-6, 100, None, None, 1, *([None, None, None, 0, 0] * 4),
+                          0, None)
+    assert rc == -1 and "multiple of 8" in abi.last_error()
+    rc = lib.qh_rmsnorm(None, None, None, 1, 0, 1e-6, None)
+    assert rc == -1 and "bad shape" in abi.last_error()
+    rc = lib.qh_gated_rmsnorm(None, None, None, None, 4, 512, 1e-6, 1, None)
+    assert rc == -1 and "head_dim" in abi.last_error()
+    rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,
+                            4096, 96, 64, 16, 4, None, 0, 1, None, None, None, 1e-6, None)
+    assert rc == -1 and "head_dim" in abi.last_error()
+    rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,
+                            4096, 256, 64, 16, 3, None, 0, 1, None, None, None, 1e-6, None)
+    assert rc == -1 and "n_kv_heads" in abi.last_error()
+    rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,
+                            16, 256, 64, 16, 4, None, 16, 1, None, None, None, 1e-6, None)
+    assert rc == -1 and "out of range" in abi.last_error()
+    rc = lib.qh_gdn_decode(None, None, None, None, None, None, None, None, None, None, None, None, None,
+                           None, 0, 16, 32, 64, 128, 1e-6, None)
+    assert rc == -1 and "dk" in abi.last_error()
+    rc = lib.qh_gemm_e4m3(None, None, None, None, 4, 4, 100, 1, 0, None, None)
+    assert rc == -1
+    # reference symbols: no error channel in the reference; ours records one
+    lib.qh_clear_error()
+    lib.launch_gemv_v4_extern(None, None, None, None, 16, 12, 1, None)
+    assert "multiple of 8" in abi.last_error()
+
+
+def test_scale_mode_encoding():
+    import torch
+    w = torch.zeros(256, 512, dtype=torch.uint8)
+    assert ops.scale_mode(w, torch.zeros(2, 4)) == 4            # block
+    assert ops.scale_mode(w, torch.zeros(256, 1)) == 1          # per row
+    assert ops.scale_mode(w, torch.zeros(256, 4)) == -4         # per row and K block
+    assert ops.scale_mode(torch.zeros(1, 128, dtype=torch.uint8), torch.zeros(1, 1)) == 1
+
+
+def test_config_shapes():
+    c = config.qwen35_4b()
+    assert c.layer_types.count("full_attention") == 8
+    assert [i for i in range(32) if c.is_full(i)] == list(range(3, 32, 4))
+    assert c.q_proj_rows == 8192 and c.kv_rows == 1024 and c.conv_dim == 8192
+    assert c.rotary_dim == 64 and c.value_dim == 4096
+    nested = {"text_config": {"hidden_size": 2560, "num_hidden_layers": 32,
+                              "rope_parameters": {"rope_theta": 1e7, "partial_rotary_factor": 0.25}}}
+    c2 = config.Qwen35Config.from_dict(nested)
+    assert c2.rope_theta == 1e7 and c2.rotary_dim == 64
+
+
+def test_engine_refuses_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    from qwen35_amd import engine, synth
+    w = synth.make_weights(config.tiny(num_layers=1, vocab=256), seed=0)
+    with pytest.raises(RuntimeError, match="needs a GPU"):
+        engine.Qwen35FP8Engine(w, max_seq_len=16)

@@ -1,0 +1,493 @@
+"""Per-kernel parity of the HIP library against the CPU oracle (MI355X only).
+
+Every call goes through the C-ABI (ctypes), the reference symbols with bf16
+scales and the native qh_* entry points with fp32 scales.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import qwen35_oracle as orc
+from qwen35_amd import abi, ops
+
+from _util import assert_close, bf, cos_sim, gen, quant, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+# Device copies made by cu() stay referenced until the test ends: a pointer
+# taken from a temporary tensor would be freed (and its memory reused by the
+# caching allocator) before the kernel reads it.
+_KEEP = []
+
+
+@pytest.fixture(autouse=True)
+def _keep_alive():
+    yield
+    torch.cuda.synchronize()
+    _KEEP.clear()
+
+
+def cu(t):
+    d = t.to(DEV).contiguous()
+    _KEEP.append(d)
+    return d
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ E4M3
+def test_e4m3_decode_all_codes(lib):
+    """Every E4M3FN code through the GEMV with s = 1 and a one-hot x equals the
+    OCP closed form (NaN codes stay NaN)."""
+    N, K = 256, 128
+    w = torch.arange(256, dtype=torch.uint8).view(N, 1).expand(N, K).contiguous()
+    s = torch.ones(N)          # one scale per row (K_blocks == 1)
+    x = torch.zeros(K, dtype=torch.bfloat16)
+    x[0] = 1.0
+    y = ops.fp8_linear(cu(x).view(1, K), cu(w), cu(s)).cpu().float()
+    ref = orc.e4m3_table()
+    nan = torch.isnan(ref)
+    assert torch.isnan(y.view(-1)[nan]).all()
+    assert torch.equal(y.view(-1)[~nan], bf(ref[~nan]).float())
+
+
+# ------------------------------------------------------------------ GEMV
+@pytest.mark.parametrize("N,K", [(256, 384), (9216, 2560), (2560, 9216), (32, 2560), (2560, 4096),
+                                 (200, 1000), (1, 128)])
+@pytest.mark.parametrize("mode", ["block", "row", "row_block"])
+def test_gemv_fp32_scales(N, K, mode):
+    g = gen(N * 7 + K)
+    W = randn(g, N, K, std=0.02)
+    if K % 128 and mode != "row":
+        pytest.skip("block scales need K % 128 == 0")
+    if mode == "block":
+        w, s = orc.quantize_block_fp8(W)
+    elif mode == "row":
+        amax = W.abs().amax(1, keepdim=True)
+        s = (amax / 448).clamp(min=1e-12)
+        w = (W / s).to(torch.float8_e4m3fn).view(torch.uint8)
+        s = s.view(N)
+    else:
+        kb = K // 128
+        blk = W.view(N, kb, 128)
+        s = (blk.abs().amax(2) / 448).clamp(min=1e-12)
+        w = (blk / s.unsqueeze(2)).to(torch.float8_e4m3fn).view(N, K).view(torch.uint8)
+    x = bf(randn(g, K))
+    code = orc.scale_code(w, s) if s.dim() == 2 else 1
+    ref = orc.linear(x.float(), orc.dequant(w, s, code))
+    lib = abi.load()
+    y = torch.empty(N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemv_e4m3(abi.ptr(cu(x)), None, None, 1e-6, K, None, None, 1,
+                               abi.ptr(cu(w)), abi.ptr(cu(s.float())), abi.ptr(y), N, code,
+                               None, None, None, 0, 0, None, None, None, 0, 0,
+                               None, None, None, 0, 0, 0, abi.stream_handle()))
+    sync()
+    assert_close(y, ref, what=f"gemv {N}x{K} {mode}")
+
+
+@pytest.mark.parametrize("N,K", [(256, 384), (9216, 2560)])
+def test_gemv_reference_abi_bf16_scales(N, K):
+    """launch_gemv_v4_extern / v3 with bf16 scale_inv, via the reference-named wrapper."""
+    g = gen(3)
+    w, s = quant(g, N, K)
+    s16 = s.to(torch.bfloat16)
+    x = bf(randn(g, K))
+    ref = orc.linear(x.float(), orc.dequant(w, s16.float()))
+    y = ops.fp8_linear(cu(x).view(1, 1, K), cu(w), cu(s16))
+    sync()
+    assert y.shape == (1, 1, N)
+    assert_close(y, ref, what="gemv bf16 scales")
+    lib = abi.load()
+    y3 = torch.empty(N, dtype=torch.bfloat16, device=DEV)
+    lib.launch_gemv_v3_extern(abi.ptr(cu(x)), abi.ptr(cu(w)), abi.ptr(cu(s16)), abi.ptr(y3),
+                              N, K, K // 128, abi.stream_handle())
+    sync()
+    assert torch.equal(y3.cpu(), y.view(-1).cpu())
+
+
+def test_grouped_projections_match_single():
+    """launch_linear_in_proj4, launch_fused_qkv and launch_fused_gate_up equal
+    separate GEMVs (one launch over concatenated row spaces)."""
+    g = gen(11)
+    K = 2560
+    segs = [quant(g, n, K) for n in (8192, 32, 32, 4096)]
+    x = bf(randn(g, K))
+    xs = cu(x)
+    lib = abi.load()
+    ys = [torch.empty(w.shape[0], dtype=torch.bfloat16, device=DEV) for w, _ in segs]
+    args = []
+    for (w, s), y in zip(segs, ys):
+        args += [abi.ptr(cu(w)), abi.ptr(cu(s.to(torch.bfloat16))), abi.ptr(y), w.shape[0], K // 128]
+    lib.qh_clear_error()
+    lib.launch_linear_in_proj4(abi.ptr(xs), *args, K, abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    for (w, s), y in zip(segs, ys):
+        ref = orc.linear(x.float(), orc.dequant(w, s.to(torch.bfloat16).float()))
+        assert_close(y, ref, what="in_proj4")
+    (wq, sq), (wk, sk), (wv, sv) = [quant(g, n, K) for n in (1024, 256, 256)]
+    q, k, v = ops.fused_qkv(xs, cu(wq), cu(sq), cu(wk), cu(sk), cu(wv), cu(sv))
+    gg, uu = ops.fused_gate_up(xs, cu(wq), cu(sq.to(torch.bfloat16)), cu(wk), cu(sk.to(torch.bfloat16)))
+    sync()
+    for y, (w, s) in ((q, (wq, sq)), (k, (wk, sk)), (v, (wv, sv))):
+        assert_close(y, orc.linear(x.float(), orc.dequant(w, s)), what="fused_qkv")
+    assert_close(gg, orc.linear(x.float(), orc.dequant(wq, sq.to(torch.bfloat16).float())), what="gate")
+    assert_close(uu, orc.linear(x.float(), orc.dequant(wk, sk.to(torch.bfloat16).float())), what="up")
+
+
+def test_gemv_norm_prologue_and_residual_epilogue():
+    g = gen(5)
+    K, N = 2560, 2560
+    w, s = quant(g, N, K)
+    x = bf(randn(g, K))
+    nw = randn(g, K, std=0.02)
+    res = bf(randn(g, N))
+    lib = abi.load()
+    y = torch.empty(N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemv_e4m3(abi.ptr(cu(x)), None, abi.ptr(cu(nw)), 1e-6, K, abi.ptr(cu(res)),
+                               None, 1, abi.ptr(cu(w)), abi.ptr(cu(s)), abi.ptr(y), N, K // 128,
+                               None, None, None, 0, 0, None, None, None, 0, 0,
+                               None, None, None, 0, 0, 0, abi.stream_handle()))
+    sync()
+    xn = orc.rmsnorm(x.float(), nw)
+    ref = orc.bf16(res.float() + orc.linear(xn, orc.dequant(w, s)))
+    assert_close(y, ref, atol_frac=1e-3, what="norm+gemv+res")
+
+
+def test_gemv_rejects_bad_args(lib):
+    y = torch.empty(8, dtype=torch.bfloat16, device=DEV)
+    rc = lib.qh_gemv_e4m3(None, None, None, 1e-6, 100, None, None, 1, None, None, abi.ptr(y), 8, 1,
+                          None, None, None, 0, 0, None, None, None, 0, 0, None, None, None, 0, 0,
+                          0, abi.stream_handle())
+    assert rc != 0 and "multiple of 8" in abi.last_error()
+
+
+# ------------------------------------------------------------------ norm
+def test_rmsnorm_reference_abi():
+    g = gen(7)
+    for N, D in ((1, 2560), (16, 256), (4, 256)):
+        x = bf(randn(g, N, D) * 3)
+        w = randn(g, D, std=0.02)
+        ref = orc.rmsnorm(x.float(), w)
+        xg = cu(x)
+        out = torch.empty_like(xg)
+        lib = abi.load()
+        lib.launch_rmsnorm_out(abi.ptr(xg), abi.ptr(cu(w)), abi.ptr(out), N, D, 1e-6, abi.stream_handle())
+        lib.launch_rmsnorm_ip(abi.ptr(xg), abi.ptr(cu(w)), N, D, 1e-6, abi.stream_handle())
+        sync()
+        assert_close(out, ref, what="rmsnorm_out")
+        assert torch.equal(xg.cpu(), out.cpu())
+
+
+# ------------------------------------------------------------------ MLP
+@pytest.mark.parametrize("H,I", [(2560, 9216), (256, 512)])
+def test_mlp_decode(H, I):
+    """fused (1+w) RMSNorm -> gate/up SiLU -> down (+residual)."""
+    g = gen(2)
+    ln = randn(g, H, std=0.02)
+    wg, sg = quant(g, I, H)
+    wu, su = quant(g, I, H)
+    wd, sd = quant(g, H, I)
+    h = bf(randn(g, H))
+    o = bf(randn(g, H))
+    ref, mref = orc.mlp_decode(h.float(), o.float(), ln, orc.dequant(wg, sg), orc.dequant(wu, su),
+                               orc.dequant(wd, sd))
+    lib = abi.load()
+    m = torch.empty(I, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_mlp_decode(abi.ptr(cu(h)), abi.ptr(cu(o)), abi.ptr(cu(ln)), 1e-6, H,
+                                abi.ptr(cu(wg)), abi.ptr(cu(sg)), abi.ptr(cu(wu)), abi.ptr(cu(su)), I,
+                                H // 128, abi.ptr(cu(wd)), abi.ptr(cu(sd)), I // 128, abi.ptr(m),
+                                abi.ptr(out), 0, abi.stream_handle()))
+    sync()
+    assert_close(m, mref, atol_frac=1e-3, what="mlp m")
+    assert_close(out, ref, atol_frac=1e-3, what="mlp out")
+
+
+def test_layer_post_o_fp8_mlp_reference_abi():
+    g = gen(9)
+    H, I = 2560, 9216
+    ln = randn(g, H, std=0.02)
+    (wg, sg), (wu, su), (wd, sd) = quant(g, I, H), quant(g, I, H), quant(g, H, I)
+    sg, su, sd = (s.to(torch.bfloat16) for s in (sg, su, sd))
+    h, o = bf(randn(g, H)), bf(randn(g, H))
+    ref, mref = orc.mlp_decode(h.float(), o.float(), ln, orc.dequant(wg, sg.float()),
+                               orc.dequant(wu, su.float()), orc.dequant(wd, sd.float()))
+    bufs = [torch.empty(n, dtype=torch.bfloat16, device=DEV) for n in (H, I, I, I, I)]
+    out, ws, gb, ub, sb = bufs
+    lib = abi.load()
+    lib.launch_rmsnorm_ip  # noqa: B018  (symbol present)
+    lib.layer_post_o_fp8_mlp(abi.ptr(cu(h)), abi.ptr(cu(o)), abi.ptr(cu(ln)), abi.ptr(cu(wg)),
+                             abi.ptr(cu(sg)), I, abi.ptr(cu(wu)), abi.ptr(cu(su)), I, abi.ptr(cu(wd)),
+                             abi.ptr(cu(sd)), H, abi.ptr(out), abi.ptr(ws), abi.ptr(gb), abi.ptr(ub),
+                             abi.ptr(sb), H, H // 128, I // 128, abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    assert_close(sb, mref, atol_frac=1e-3, what="silu_buf")
+    assert_close(out, ref, atol_frac=1e-3, what="post_o_mlp")
+
+
+# ------------------------------------------------------------------ attention
+def _attn_case(g, ctx, Hq=16, Hkv=4, D=256, rot=64, max_seq=None):
+    max_seq = max_seq or ctx
+    kc = bf(randn(g, Hkv, max_seq, D)).float()
+    vc = bf(randn(g, Hkv, max_seq, D)).float()
+    q_all = bf(randn(g, Hq * 2 * D))
+    k_new = bf(randn(g, Hkv * D))
+    v_new = bf(randn(g, Hkv * D))
+    qn = randn(g, D, std=0.02)
+    kn = randn(g, D, std=0.02)
+    return kc, vc, q_all, k_new, v_new, qn, kn
+
+
+@pytest.mark.parametrize("ctx,splits", [(1, 1), (17, 1), (130, 4), (4096, 32), (427, 32)])
+def test_attn_decode(ctx, splits):
+    """BASELINE config 4b (ctx 4096): q/k norm, partial RoPE (theta 1e7, 64 of
+    256 dims), KV write at slot ctx-1, GQA 16/4, sigmoid gate."""
+    g = gen(ctx)
+    Hq, Hkv, D, rot, max_seq = 16, 4, 256, 64, 4096
+    kc, vc, q_all, k_new, v_new, qn, kn = _attn_case(g, ctx, max_seq=max_seq)
+    cos, sin = orc.rope_tables(max_seq, rot, 1e7)
+    pos = ctx - 1
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    ref = orc.attn_decode(q_all.float(), k_new.float(), v_new.float(), qn, kn, cos, sin, kc_ref,
+                          vc_ref, pos, Hq, Hkv, D, rot)
+    lib = abi.load()
+    kcg, vcg = cu(bf(kc)), cu(bf(vc))
+    out = torch.empty(Hq * D, dtype=torch.bfloat16, device=DEV)
+    scratch = torch.zeros(int(lib.qh_attn_scratch_bytes(Hkv, splits, D)) + 4, dtype=torch.uint8, device=DEV)
+    counters = torch.zeros(Hkv, dtype=torch.int32, device=DEV)
+    posd = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    qa = cu(q_all)
+    for use_dev_pos in (True, False):
+        abi.check(lib.qh_attn_decode(abi.ptr(qa), 2 * D, abi.ptr(qa[D:]), 2 * D, abi.ptr(cu(k_new)),
+                                     abi.ptr(cu(v_new)), abi.ptr(cu(qn)), abi.ptr(cu(kn)), abi.ptr(cu(cos)),
+                                     abi.ptr(cu(sin)), abi.ptr(kcg), abi.ptr(vcg), max_seq, D, rot, Hq, Hkv,
+                                     abi.ptr(posd) if use_dev_pos else None, pos, splits,
+                                     abi.ptr(scratch), abi.ptr(counters), abi.ptr(out), 1e-6,
+                                     abi.stream_handle()))
+        sync()
+        assert_close(out, ref, atol_frac=1e-3, what=f"attn ctx={ctx} splits={splits}")
+        assert torch.equal(kcg[:, pos].cpu().float(), kc_ref[:, pos]), "K cache slot"
+        assert torch.equal(vcg[:, pos].cpu().float(), vc_ref[:, pos]), "V cache slot"
+        assert int(counters.abs().sum()) == 0, "arrival counters must self-reset"
+
+
+def test_layer_mid_attn_reference_abi():
+    g = gen(21)
+    Hq, Hkv, D, rot, max_seq, past = 16, 4, 256, 64, 512, 99
+    kc, vc, q_all, k_new, v_new, qn, kn = _attn_case(g, past + 1, max_seq=max_seq)
+    cos, sin = orc.rope_tables(max_seq, rot, 1e7)
+    q = q_all.float().view(Hq, 2 * D)[:, :D].reshape(-1)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    qr = orc.rope_rows(orc.rmsnorm(q.view(Hq, D), qn), cos[past], sin[past], rot, True)
+    kr = orc.rope_rows(orc.rmsnorm(k_new.float().view(Hkv, D), kn), cos[past], sin[past], rot, True)
+    kc_ref[:, past] = kr
+    vc_ref[:, past] = v_new.float().view(Hkv, D)
+    ref = orc.attn_only(qr, kc_ref, vc_ref, past + 1, Hq, Hkv)
+    lib = abi.load()
+    qb, kb = cu(bf(q)), cu(k_new)
+    kcg, vcg = cu(bf(kc)), cu(bf(vc))
+    out = torch.empty(Hq * D, dtype=torch.bfloat16, device=DEV)
+    lib.layer_mid_attn(abi.ptr(qb), abi.ptr(kb), abi.ptr(cu(v_new)), abi.ptr(out), abi.ptr(cu(qn)),
+                       abi.ptr(cu(kn)), abi.ptr(cu(cos)), abi.ptr(cu(sin)), abi.ptr(kcg), abi.ptr(vcg),
+                       past, past, past + 1, max_seq, D, rot, Hq, Hkv, abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    assert_close(out, ref, atol_frac=1e-3, what="layer_mid_attn")
+    assert torch.equal(qb.cpu().float().view(Hq, D), qr), "q written back normalised + rotated"
+    assert torch.equal(kb.cpu().float().view(Hkv, D), kr)
+    # launch_fused_attn_v2 on the updated cache with the rotated q
+    out2 = torch.empty_like(out)
+    lib.launch_fused_attn_v2(abi.ptr(qb), abi.ptr(kcg), abi.ptr(vcg), abi.ptr(out2), past + 1, max_seq,
+                             D, Hq, Hkv, abi.stream_handle())
+    sync()
+    assert_close(out2, ref, atol_frac=1e-3, what="fused_attn_v2")
+
+
+# ------------------------------------------------------------------ GDN
+def _gdn_inputs(g, Hk=16, Hv=32, dk=128, dv=128):
+    C = 2 * Hk * dk + Hv * dv
+    return dict(
+        mixed=bf(randn(g, C)), a=bf(randn(g, Hv)), b=bf(randn(g, Hv)), z=bf(randn(g, Hv * dv)),
+        conv_state=bf(randn(g, C, 4, std=1.0)), conv_w=bf(randn(g, C, 4, std=0.5)),
+        A_log=torch.log(1e-3 + torch.rand(Hv, generator=g) * 16), dt_bias=torch.ones(Hv),
+        norm_w=bf(1 + randn(g, dv, std=0.02)), S=randn(g, Hv, dk, dv, std=0.1))
+
+
+def _ring_from_ordered(state, t):
+    """Ordered conv state [C, 4] (oldest..newest = x_{t-4..t-1}) -> ring with
+    slot j holding x_j mod 4."""
+    ring = torch.empty_like(state)
+    for i in range(4):
+        ring[:, (t - 4 + i) % 4] = state[:, i]
+    return ring
+
+
+@pytest.mark.parametrize("t", [7, 4096])
+def test_gdn_decode(t):
+    """BASELINE config 4a: conv update + gates + l2norm + delta rule + gated RMSNorm."""
+    g = gen(t)
+    Hk, Hv, dk, dv = 16, 32, 128, 128
+    d = _gdn_inputs(g, Hk, Hv, dk, dv)
+    kd = Hk * dk
+    st = d["conv_state"].float().clone()
+    y = orc.conv_update(d["mixed"].float(), st, d["conv_w"].float())
+    q = y[:kd].view(Hk, dk).repeat_interleave(2, 0)
+    k = y[kd:2 * kd].view(Hk, dk).repeat_interleave(2, 0)
+    v = y[2 * kd:].view(Hv, dv)
+    gg, beta = orc.linear_gates(d["a"].float(), d["b"].float(), d["A_log"], d["dt_bias"])
+    S = d["S"].clone()
+    core = orc.delta_rule_step(q, k, v, gg, beta, S)
+    ref = orc.gated_rmsnorm(core, d["z"].float().view(Hv, dv), d["norm_w"].float())
+    lib = abi.load()
+    ring = cu(bf(_ring_from_ordered(d["conv_state"].float(), t)))
+    Sg = cu(d["S"])
+    coreg = torch.empty(Hv * dv, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(Hv * dv, dtype=torch.bfloat16, device=DEV)
+    counters = torch.zeros(Hv, dtype=torch.int32, device=DEV)
+    abi.check(lib.qh_gdn_decode(abi.ptr(cu(d["mixed"])), abi.ptr(cu(d["a"])), abi.ptr(cu(d["b"])),
+                                abi.ptr(cu(d["z"])), abi.ptr(ring), abi.ptr(cu(d["conv_w"])),
+                                abi.ptr(cu(d["A_log"])), abi.ptr(cu(d["dt_bias"])), abi.ptr(cu(d["norm_w"])),
+                                abi.ptr(Sg), abi.ptr(coreg), abi.ptr(out), abi.ptr(counters), None, t,
+                                Hk, Hv, dk, dv, 1e-6, abi.stream_handle()))
+    sync()
+    assert_close(coreg, core, atol_frac=1e-3, what="gdn core")
+    assert_close(out, ref, atol_frac=2e-3, what="gdn gated out")
+    c = cos_sim(Sg.cpu(), S)
+    assert c > 0.999999, f"state cosine {c}"
+    assert torch.allclose(Sg.cpu(), S, rtol=1e-4, atol=1e-5)
+    assert torch.equal(ring.cpu().float(), _ring_from_ordered(st, t + 1)), "conv ring update"
+    assert int(counters.abs().sum()) == 0
+
+
+def test_delta_rule_and_gates_reference_abi():
+    g = gen(31)
+    H, hd = 32, 128
+    q, k, v = bf(randn(g, H, hd)), bf(randn(g, H, hd)), bf(randn(g, H, hd))
+    a, b = bf(randn(g, H)), bf(randn(g, H))
+    A_log = torch.log(1e-3 + torch.rand(H, generator=g) * 16)
+    dt = torch.ones(H)
+    gg, beta = orc.linear_gates(a.float(), b.float(), A_log, dt)
+    S = randn(g, H, hd, hd, std=0.1)
+    Sr = S.clone()
+    ref = orc.delta_rule_step(q.float(), k.float(), v.float(), gg, beta, Sr)
+    lib = abi.load()
+    gd = torch.empty(H, device=DEV)
+    bd = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    lib.launch_prepare_linear_gates(abi.ptr(cu(a)), abi.ptr(cu(b)), abi.ptr(cu(A_log)), abi.ptr(cu(dt)),
+                                    abi.ptr(gd), abi.ptr(bd), H, abi.stream_handle())
+    Sg = cu(S)
+    out = torch.empty(H * hd, dtype=torch.bfloat16, device=DEV)
+    lib.launch_delta_rule_decode(abi.ptr(cu(q)), abi.ptr(cu(k)), abi.ptr(cu(v)), abi.ptr(gd), abi.ptr(bd),
+                                 abi.ptr(Sg), abi.ptr(out), H, hd, abi.stream_handle())
+    z = bf(randn(g, H * hd))
+    w = bf(1 + randn(g, hd, std=0.02))
+    gated = torch.empty_like(out)
+    lib.launch_rmsnorm_gated_decode(abi.ptr(out), abi.ptr(cu(z)), abi.ptr(cu(w)), abi.ptr(gated), H, hd,
+                                    1e-6, abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    assert torch.allclose(gd.cpu(), gg, rtol=1e-5, atol=1e-6)
+    assert torch.equal(bd.cpu().float(), beta)
+    assert_close(out, ref, atol_frac=1e-3, what="delta rule")
+    assert torch.allclose(Sg.cpu(), Sr, rtol=1e-4, atol=1e-5)
+    gref = orc.gated_rmsnorm(out.cpu().float().view(H, hd), z.float().view(H, hd), w.float(), bf16_steps=False)
+    assert_close(gated, gref, atol_frac=1e-3, what="rmsnorm_gated_decode")
+
+
+# ------------------------------------------------------------------ lm_head
+@pytest.mark.parametrize("V,K", [(1000, 256), (248320, 2560)])
+def test_lm_head_argmax(V, K):
+    g = gen(V)
+    W = bf(randn(g, V, K, std=0.02))
+    h = bf(randn(g, K) * 4)
+    nf = randn(g, K, std=0.02)
+    logits_ref, tok_ref = orc.lm_head_argmax(h.float(), nf, W.float())
+    lib = abi.load()
+    logits = torch.empty(V, dtype=torch.bfloat16, device=DEV)
+    scratch = torch.zeros(int(lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8, device=DEV)
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tok = torch.zeros(1, dtype=torch.int64, device=DEV)
+    hist = torch.full((8,), -1, dtype=torch.int64, device=DEV)
+    pos = torch.tensor([3], dtype=torch.int32, device=DEV)
+    emb = cu(W)
+    nxt = torch.empty(K, dtype=torch.bfloat16, device=DEV)
+    for rep in range(2):
+        abi.check(lib.qh_lm_head_argmax(abi.ptr(cu(h)), abi.ptr(cu(nf)), 1e-6, K, abi.ptr(cu(W)), V,
+                                        abi.ptr(logits), abi.ptr(scratch), abi.ptr(counter), abi.ptr(tok),
+                                        abi.ptr(hist), 8, abi.ptr(pos), abi.ptr(emb), abi.ptr(nxt),
+                                        abi.stream_handle()))
+    sync()
+    assert_close(logits, logits_ref, atol_frac=1e-3, what="logits")
+    got = int(tok.item())
+    lg = logits.cpu().float()
+    assert got == orc.argmax_first(lg), "argmax of the GPU's own bf16 logits"
+    if got != tok_ref:  # only allowed on a bf16 near-tie
+        assert abs(float(logits_ref[got]) - float(logits_ref[tok_ref])) <= 2 ** -7 * abs(float(logits_ref[tok_ref]))
+    assert int(pos.item()) == 5 and int(hist[3]) == got and int(hist[4]) == got
+    assert torch.equal(nxt.cpu(), W[got])
+    assert int(counter.item()) == 0
+
+
+def test_argmax_ties_lowest_index():
+    V, K = 4096, 128
+    W = torch.zeros(V, K, dtype=torch.bfloat16)
+    for r in (4000, 77, 2048, 3999):
+        W[r, 0] = 1.0
+    h = torch.zeros(K, dtype=torch.bfloat16)
+    h[0] = 1.0
+    lib = abi.load()
+    logits = torch.empty(V, dtype=torch.bfloat16, device=DEV)
+    scratch = torch.zeros(int(lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8, device=DEV)
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tok = torch.zeros(1, dtype=torch.int64, device=DEV)
+    abi.check(lib.qh_lm_head_argmax(abi.ptr(cu(h)), None, 1e-6, K, abi.ptr(cu(W)), V, abi.ptr(logits),
+                                    abi.ptr(scratch), abi.ptr(counter), abi.ptr(tok), None, 0, None, None,
+                                    None, abi.stream_handle()))
+    sync()
+    assert int(tok.item()) == 77
+
+
+def test_argmax_nan_logits_stay_in_bounds():
+    """Regression: all-NaN logits once left the argmax at its INT_MAX sentinel
+    and the next-token embedding copy read far out of bounds.  NaN now ranks
+    highest (torch.argmax order) and the index is clamped into the vocabulary."""
+    V, K = 1000, 128
+    W = torch.ones(V, K, dtype=torch.bfloat16)
+    W[5:, 0] = float("nan")
+    h = torch.ones(K, dtype=torch.bfloat16)
+    lib = abi.load()
+    logits = torch.empty(V, dtype=torch.bfloat16, device=DEV)
+    scratch = torch.zeros(int(lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8, device=DEV)
+    counter = torch.zeros(1, dtype=torch.int32, device=DEV)
+    tok = torch.zeros(1, dtype=torch.int64, device=DEV)
+    emb, nxt = cu(W), torch.empty(K, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_lm_head_argmax(abi.ptr(cu(h)), None, 1e-6, K, abi.ptr(emb), V, abi.ptr(logits),
+                                    abi.ptr(scratch), abi.ptr(counter), abi.ptr(tok), None, 0, None,
+                                    abi.ptr(emb), abi.ptr(nxt), abi.stream_handle()))
+    sync()
+    assert int(tok.item()) == 5
+
+
+# ------------------------------------------------------------------ prefill GEMM
+@pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256)])
+def test_gemm_e4m3(M, N, K):
+    """BASELINE config 3a: X bf16 [M, K] . deq(W)^T through the fp8 matrix cores."""
+    g = gen(M + N + K)
+    w, s = quant(g, N, K)
+    x = bf(randn(g, M, K))
+    ref = x.float() @ orc.dequant(w, s).t()
+    y = ops.fp8_linear(cu(x), cu(w), cu(s))
+    sync()
+    c = cos_sim(y.cpu().float(), ref)
+    assert c >= 0.99999, f"gemm cosine {c}"
+    assert_close(y, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="gemm")
+    y16 = ops.fp8_linear(cu(x), cu(w), cu(s.to(torch.bfloat16)))   # reference symbol fp8_gemm_batch
+    sync()
+    ref16 = x.float() @ orc.dequant(w, s.to(torch.bfloat16).float()).t()
+    assert cos_sim(y16.cpu().float(), ref16) >= 0.99999
