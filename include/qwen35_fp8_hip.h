@@ -175,7 +175,8 @@ int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_strid
 
 /* GatedDeltaNet decode step: causal conv update (4-slot ring indexed by
  * position), gates, l2norm, delta rule (state in place), gated RMSNorm
- * (main.py:1064-1162 with launch_delta_rule_decode semantics). */
+ * (main.py:1064-1162 with launch_delta_rule_decode semantics).  `core` is an
+ * fp32 scratch of Hv*dv floats; `counters` Hv zero-initialised uints. */
 int qh_gdn_decode(const void* mixed, const void* a, const void* b, const void* z,
                   void* conv_ring, const void* conv_w, const float* A_log, const float* dt_bias,
                   const void* norm_w, float* state, void* core, void* out, unsigned* counters,

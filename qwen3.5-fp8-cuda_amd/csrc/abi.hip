@@ -508,7 +508,7 @@ QH_EXPORT int qh_gdn_decode(const void* mixed, const void* a, const void* b, con
   g.dt_bias = dt_bias;
   g.norm_w = (const uint16_t*)norm_w;
   g.state = state;
-  g.core = (uint16_t*)core;
+  g.core = (float*)core;
   g.out = (uint16_t*)out;
   g.counters = counters;
   g.pos_dev = pos_dev;

@@ -116,6 +116,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   const float* cos_row = p.cos_t + (size_t)rope_pos * p.rot;
   const float* sin_row = p.sin_t + (size_t)rope_pos * p.rot;
   const float scale = rsqrtf((float)D);
+  const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
+  const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
+  const bool new_kv = p.k_new != nullptr;
+
+  // K/V tile staging: each thread moves PER 16-byte pieces of K and of V.
+  // Loads are branch-free (clamped to a valid row) so a whole tile is in
+  // flight at once; the next tile is requested before the current one is used.
+  constexpr int PER = TP * (D / 8) / 256;
+  u32x4 kreg[PER], vreg[PER];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int idx = threadIdx.x + 256 * e;
+      const int pos = t0 + idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const int src = pos < p1 ? pos : t0;
+      kreg[e] = *(const u32x4*)(kbase + (size_t)src * D + c8);
+      vreg[e] = *(const u32x4*)(vbase + (size_t)src * D + c8);
+    }
+  };
+  auto stage = [&](int t0) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int idx = threadIdx.x + 256 * e;
+      const int row = idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const int pos = t0 + row;
+      u32x4 kq = kreg[e], vq = vreg[e];
+      if (new_kv && pos == slot) {
+        kq = *(const u32x4*)(sKn + c8);
+        vq = *(const u32x4*)(sVn + c8);
+      }
+      if (pos >= p1) { kq = zero; vq = zero; }
+      *(u32x4*)(sK + row * KS + c8) = kq;
+      *(u32x4*)(sV + row * D + c8) = vq;
+    }
+  };
+  if (p0 < p1) fetch(p0);
 
   // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
   for (int gi = wid; gi < G; gi += 4) {
@@ -151,29 +190,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
 #pragma unroll
     for (int i = 0; i < NPL; ++i) o[hi][i] = 0.0f;
   }
-  const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
-  const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
-  const bool new_kv = p.k_new != nullptr;
 
   for (int t0 = p0; t0 < p1; t0 += TP) {
-    for (int idx = threadIdx.x; idx < TP * (D / 8); idx += 256) {
-      const int row = idx / (D / 8);
-      const int c8 = (idx % (D / 8)) * 8;
-      const int pos = t0 + row;
-      u32x4 kq = {0u, 0u, 0u, 0u}, vq = {0u, 0u, 0u, 0u};
-      if (pos < p1) {
-        if (new_kv && pos == slot) {
-          kq = *(const u32x4*)(sKn + c8);
-          vq = *(const u32x4*)(sVn + c8);
-        } else {
-          kq = *(const u32x4*)(kbase + (size_t)pos * D + c8);
-          vq = *(const u32x4*)(vbase + (size_t)pos * D + c8);
-        }
-      }
-      *(u32x4*)(sK + row * KS + c8) = kq;
-      *(u32x4*)(sV + row * D + c8) = vq;
-    }
+    stage(t0);
     __syncthreads();
+    if (t0 + TP < p1) fetch(t0 + TP);
 
     // scores: lane pair (2j, 2j+1) owns position t0+j, each lane half the dims
     const int prow = lane >> 1, half = lane & 1;
@@ -256,50 +277,40 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     if (gi < G) {
       float* dst = p.part + ((size_t)(kvh * p.nsplit + split) * MAXG + gi) * rec;
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) dst[lane * NPL + i] = o[hi][i];
-      if (lane == 0) { dst[D] = m[hi]; dst[D + 1] = l[hi]; }
+      for (int i = 0; i < NPL; ++i) pub_store(dst + lane * NPL + i, o[hi][i]);
+      if (lane == 0) {
+        pub_store(dst + D, m[hi]);
+        pub_store(dst + D + 1, l[hi]);
+      }
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(p.counters + kvh, 1u);
-    s_last = prev == (unsigned)(p.nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(p.counters + kvh, (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
     const int gi = wid + 4 * hi;
     if (gi >= G) continue;
-    float M = -INFINITY;
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float* src = p.part + ((size_t)(kvh * p.nsplit + s) * MAXG + gi) * rec;
-      const float ls = __hip_atomic_load(src + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float ms = __hip_atomic_load(src + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (ls > 0.0f) M = fmaxf(M, ms);
-    }
-    float L = 0.0f, acc[NPL];
+    const float* base = p.part + ((size_t)kvh * p.nsplit * MAXG + gi) * rec;
+    const size_t sstride = (size_t)MAXG * rec;
+    // lane s holds split s's (m, l); nsplit <= 64 (checked on the host)
+    const bool have = lane < p.nsplit;
+    const float ls = have ? pub_load(base + lane * sstride + D + 1) : 0.0f;
+    const float ms = have ? pub_load(base + lane * sstride + D) : -INFINITY;
+    const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
+    const float ws = ls > 0.0f ? __expf(ms - M) : 0.0f;
+    const float L = wave_sum(ls * ws);
+    float acc[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
     for (int s = 0; s < p.nsplit; ++s) {
-      const float* src = p.part + ((size_t)(kvh * p.nsplit + s) * MAXG + gi) * rec;
-      const float ls = __hip_atomic_load(src + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (!(ls > 0.0f)) continue;
-      const float ms = __hip_atomic_load(src + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float w = __expf(ms - M);
-      L = fmaf(ls, w, L);
+      const float w = __shfl(ws, s, 64);
+      if (w == 0.0f) continue;  // uniform: empty split
+      const float* src = base + s * sstride + lane * NPL;
 #pragma unroll
-      for (int i = 0; i < NPL; ++i)
-        acc[i] = fmaf(__hip_atomic_load(src + lane * NPL + i, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT),
-                      w, acc[i]);
+      for (int i = 0; i < NPL; ++i) acc[i] = fmaf(pub_load(src + i), w, acc[i]);
     }
     emit(gi, acc, 1.0f / L);
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(p.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) reset_counter(p.counters + kvh);
 }
 
 }  // namespace
@@ -324,8 +335,8 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
     qh_set_error("attn: rotary_dim=%d unsupported for head_dim=%d", p.rot, head_dim);
     return -1;
   }
-  if (p.nsplit < 1 || (p.nsplit > 1 && (!p.part || !p.counters))) {
-    qh_set_error("attn: split-K needs scratch and counters");
+  if (p.nsplit < 1 || p.nsplit > 64 || (p.nsplit > 1 && (!p.part || !p.counters))) {
+    qh_set_error("attn: nsplit=%d must be 1..64; split-K needs scratch and counters", p.nsplit);
     return -1;
   }
   if (!p.pos_dev) {

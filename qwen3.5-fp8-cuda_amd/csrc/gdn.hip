@@ -29,21 +29,27 @@ namespace {
 constexpr int VS = 32;  // value columns per workgroup
 
 // Delta-rule update of 32 value columns.  Thread t: column t & 31, rows
-// (t >> 5) * DK/8 .. +DK/8.  qn/kn: normalised q, k (fp32, LDS).
+// (t >> 5) * DK/8 .. +DK/8 (S holds them, loaded early by load_columns).
+// qn/kn: normalised q, k (fp32, LDS).  Returns the column's output o.
 template <int DK>
-__device__ __forceinline__ float delta_columns(float* state_cols, int dv, const float* qn,
-                                               const float* kn, float vval, float beta,
-                                               float decay, float* red) {
+__device__ __forceinline__ void load_columns(float (&S)[DK / 8], const float* state_cols, int dv) {
   constexpr int RPT = DK / 8;
   const int j = threadIdx.x & 31;
   const int rg = threadIdx.x >> 5;
-  float S[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) S[r] = state_cols[(size_t)(rg * RPT + r) * dv + j];
+}
+
+template <int DK>
+__device__ __forceinline__ float delta_columns(const float (&S)[DK / 8], float* state_cols, int dv,
+                                               const float* qn, const float* kn, float vval,
+                                               float beta, float decay, float* red) {
+  constexpr int RPT = DK / 8;
+  const int j = threadIdx.x & 31;
+  const int rg = threadIdx.x >> 5;
   float pred = 0.0f;
 #pragma unroll
-  for (int r = 0; r < RPT; ++r) {
-    S[r] = state_cols[(size_t)(rg * RPT + r) * dv + j];
-    pred = fmaf(S[r] * decay, kn[rg * RPT + r], pred);
-  }
+  for (int r = 0; r < RPT; ++r) pred = fmaf(S[r] * decay, kn[rg * RPT + r], pred);
   red[rg * 32 + j] = pred;
   __syncthreads();
   pred = 0.0f;
@@ -92,6 +98,10 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
   const int t = p.pos_dev ? *p.pos_dev : p.pos;
   const int dv = p.dv;
   const int tid = threadIdx.x;
+  // The state columns are the bulk of the traffic: request them first.
+  float* cols = p.state + (size_t)h * DK * dv + sidx * VS;
+  float S[DK / 8];
+  load_columns<DK>(S, cols, dv);
 
   // ---- causal conv (window of 4) + SiLU for q/k of key head kh ------------
   {
@@ -129,35 +139,22 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
   const float decay = __expf(g);
   __syncthreads();
 
-  float* cols = p.state + (size_t)h * DK * dv + sidx * VS;
-  const float o = delta_columns<DK>(cols, dv, qn, kn, vconv[tid & 31], beta, decay, red);
+  const float o = delta_columns<DK>(S, cols, dv, qn, kn, vconv[tid & 31], beta, decay, red);
   const int j = tid & 31;
-  if (tid < 32) p.core[(size_t)h * dv + sidx * VS + j] = f2bf(o);
+  // core = bf16(o), published as fp32 for the head's last column workgroup
+  if (tid < 32) pub_store(p.core + (size_t)h * dv + sidx * VS + j, rbf(o));
 
   // ---- gated RMSNorm by the last column workgroup of this head ------------
   const int nslice = dv / VS;
   if (nslice > 1) {
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = atomicAdd(p.counters + h, 1u);
-      s_last = prev == (unsigned)(nslice - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!arrive_last(p.counters + h, (unsigned)nslice, &s_last)) return;
   } else {
+    wait_mem();
     __syncthreads();
   }
   // dv <= 256: one element per thread
   const bool ok = tid < dv;
-  float x = 0.0f;
-  if (ok) {
-    const uint16_t* src = p.core + (size_t)h * dv + tid;
-    const uint32_t word = __hip_atomic_load((const uint32_t*)((uintptr_t)src & ~(uintptr_t)3),
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    x = (tid & 1) ? bf_hi(word) : bf_lo(word);
-  }
+  const float x = ok ? pub_load(p.core + (size_t)h * dv + tid) : 0.0f;
   float ss = wave_sum(x * x);
   __syncthreads();
   if ((tid & 63) == 0) red2[tid >> 6] = ss;
@@ -169,8 +166,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
     const float sz = rbf(qh_silu(bf2f(p.z[(size_t)h * dv + tid])));
     p.out[(size_t)h * dv + tid] = f2bf(normed * sz);
   }
-  if (nslice > 1 && tid == 0)
-    __hip_atomic_store(p.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (nslice > 1 && tid == 0) reset_counter(p.counters + h);
 }
 
 // Reference ABI delta rule (fused_kernels.cu:623-684): q, k already expanded to
@@ -211,7 +207,9 @@ __global__ __launch_bounds__(256) void delta_rule_kernel(const uint16_t* q, cons
   const int j = tid & 31;
   const float vval = bf2f(v[(size_t)h * DK + sidx * VS + j]);
   float* cols = state + (size_t)h * DK * DK + sidx * VS;
-  const float o = delta_columns<DK>(cols, DK, qn, kn, vval, bt, decay, red);
+  float S[DK / 8];
+  load_columns<DK>(S, cols, DK);
+  const float o = delta_columns<DK>(S, cols, DK, qn, kn, vval, bt, decay, red);
   if (tid < 32) out[(size_t)h * DK + sidx * VS + j] = f2bf(o);
 }
 

@@ -48,9 +48,7 @@ __device__ __forceinline__ float sumsq_bf16x8(u32x4 a, float s) {
 }
 
 // y = bf16((x * rms) * (1 + w)) for 8 elements (reference order, fused_kernels.cu:545).
-__device__ __forceinline__ u32x4 norm_bf16x8(u32x4 a, float rms, const float* w) {
-  const f32x4 w0 = *(const f32x4*)w;
-  const f32x4 w1 = *(const f32x4*)(w + 4);
+__device__ __forceinline__ u32x4 norm_bf16x8(u32x4 a, float rms, f32x4 w0, f32x4 w1) {
   u32x4 r;
   r.x = pack_bf2(bf_lo(a.x) * rms * (1.0f + w0.x), bf_hi(a.x) * rms * (1.0f + w0.y));
   r.y = pack_bf2(bf_lo(a.y) * rms * (1.0f + w0.z), bf_hi(a.y) * rms * (1.0f + w0.w));
@@ -60,22 +58,38 @@ __device__ __forceinline__ u32x4 norm_bf16x8(u32x4 a, float rms, const float* w)
 }
 
 // Loads this lane's activation slice (chunks lane + 64*j) and applies the
-// optional add / RMSNorm prologue.  Chunks past K read as zero.
+// optional add / RMSNorm prologue.  Chunks past K read as zero.  Every load is
+// issued unconditionally from a clamped address, so they are all in flight at
+// once (no per-chunk branch, no per-chunk wait).
 template <int CPL>
 __device__ __forceinline__ void load_x_slice(u32x4 (&xr)[CPL], const uint16_t* x,
                                              const uint16_t* x2, const float* norm_w,
                                              float eps, int K, int lane) {
+  bool ok[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
-    u32x4 a = {0u, 0u, 0u, 0u};
-    if (c * 8 < K) {
-      a = *(const u32x4*)(x + c * 8);
-      if (x2) a = add_bf16x8(a, *(const u32x4*)(x2 + c * 8));
-    }
-    xr[j] = a;
+    ok[j] = c * 8 < K;
+    xr[j] = *(const u32x4*)(x + (ok[j] ? c : 0) * 8);
   }
+  if (x2) {
+    u32x4 b[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) b[j] = *(const u32x4*)(x2 + (ok[j] ? lane + 64 * j : 0) * 8);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) xr[j] = add_bf16x8(xr[j], b[j]);
+  }
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) xr[j] = ok[j] ? xr[j] : zero;
   if (norm_w) {
+    f32x4 w0[CPL], w1[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float* wp = norm_w + (ok[j] ? lane + 64 * j : 0) * 8;
+      w0[j] = *(const f32x4*)wp;
+      w1[j] = *(const f32x4*)(wp + 4);
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) ss = sumsq_bf16x8(xr[j], ss);
@@ -83,25 +97,80 @@ __device__ __forceinline__ void load_x_slice(u32x4 (&xr)[CPL], const uint16_t* x
     const float rms = rsqrtf(ss / (float)K + eps);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      if (c * 8 < K) xr[j] = norm_bf16x8(xr[j], rms, norm_w + c * 8);
+      const u32x4 n = norm_bf16x8(xr[j], rms, w0[j], w1[j]);
+      xr[j] = ok[j] ? n : zero;
     }
   }
 }
 
-template <int R>
-__device__ __forceinline__ float pick_lane(const float (&acc)[R], int lane) {
-  float v = acc[0];
+// Loads R rows of this lane's weight chunks (non-temporal) and the matching
+// fp32 scales; chunks past K get zero weights and a zero scale.
+template <int CPL, int R, typename ScaleT>
+__device__ __forceinline__ void load_rows(u32x2 (&wr)[R][CPL], float (&sc)[R][CPL],
+                                          const uint8_t* w, const ScaleT* s, int kb, int n,
+                                          int row0, int K, int lane) {
 #pragma unroll
-  for (int r = 1; r < R; ++r)
-    if (lane == r) v = acc[r];
-  return v;
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, n - 1);
+    const uint8_t* wrow = w + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      wr[r][j] = ld_w8(wrow + (c * 8 < K ? c : 0) * 8);
+    }
+  }
+  if (kb > 1) {
+    // 128x128 block scales: the R rows (R divides 128) share one row block.
+    const ScaleT* srow = s + (row0 >> 7) * kb;
+    float b[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      b[j] = load_scale<ScaleT>(srow, c * 8 < K ? (c >> 4) : 0);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) sc[r][j] = b[j];
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = min(row0 + r, n - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        sc[r][j] = load_scale<ScaleT>(s, scale_index(kb, row, c * 8 < K ? (c >> 4) : 0));
+      }
+    }
+  }
+  const u32x2 z = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const bool ok = (lane + 64 * j) * 8 < K;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wr[r][j] = ok ? wr[r][j] : z;
+      sc[r][j] = ok ? sc[r][j] : 0.0f;
+    }
+  }
+}
+
+template <int CPL, int R>
+__device__ __forceinline__ void dot_rows(float (&acc)[R], const u32x2 (&wr)[R][CPL],
+                                         const float (&sc)[R][CPL], const u32x4 (&xr)[CPL]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      acc[r] = fmaf(dot8_e4m3_bf16(wr[r][j].x, wr[r][j].y, xr[j], 0.0f), sc[r][j], acc[r]);
+  }
 }
 
 template <int CPL, int R, typename ScaleT>
 __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
   u32x4 xr[CPL];
   load_x_slice<CPL>(xr, p.x, p.x2, p.norm_w, p.eps, K, lane);
@@ -115,61 +184,30 @@ __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
     const int row0 = (g - p.gstart[si]) * R;
 
     u32x2 wr[R][CPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, sg.n - 1);
-      const uint8_t* wrow = sg.w + (size_t)row * K;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        wr[r][j] = (c * 8 < K) ? ld_w8(wrow + c * 8) : u32x2{0u, 0u};
-      }
-    }
-
+    float sc[R][CPL];
+    load_rows<CPL, R, ScaleT>(wr, sc, sg.w, (const ScaleT*)sg.s, sg.kb, sg.n, row0, K, lane);
     float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    const ScaleT* s = (const ScaleT*)sg.s;
-    if (sg.kb > 1) {
-      // 128x128 block scales: the R rows share one 128-row block.
-      const ScaleT* srow = s + (row0 >> 7) * sg.kb;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        if (c * 8 < K) {
-          const float sc = load_scale<ScaleT>(srow, c >> 4);
-#pragma unroll
-          for (int r = 0; r < R; ++r)
-            acc[r] = fmaf(dot8_e4m3_bf16(wr[r][j].x, wr[r][j].y, xr[j], 0.0f), sc, acc[r]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = min(row0 + r, sg.n - 1);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-          const int c = lane + 64 * j;
-          if (c * 8 < K) {
-            const float sc = load_scale<ScaleT>(s, scale_index(sg.kb, row, c >> 4));
-            acc[r] = fmaf(dot8_e4m3_bf16(wr[r][j].x, wr[r][j].y, xr[j], 0.0f), sc, acc[r]);
-          }
-        }
-      }
-    }
+    dot_rows<CPL, R>(acc, wr, sc, xr);
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
 
-    const float v = pick_lane<R>(acc, lane);
-    const int row = row0 + lane;
-    if (lane < R && row < sg.n) {
-      float y = rbf(v);
-      if (p.res1) {
-        float res = bf2f(p.res1[row]);
-        if (p.res2) res = rbf(res + bf2f(p.res2[row]));
-        y = res + y;
+    // Every lane holds every row total after the butterfly; lane 0 stores
+    // them with static indices (a lane-indexed pick would be lowered to a
+    // dynamically indexed array spilled through LDS).
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row < sg.n) {
+          float y = rbf(acc[r]);
+          if (p.res1) {
+            float res = bf2f(p.res1[row]);
+            if (p.res2) res = rbf(res + bf2f(p.res2[row]));
+            y = res + y;
+          }
+          sg.y[row] = f2bf(y);
+        }
       }
-      sg.y[row] = f2bf(y);
     }
   }
 }
@@ -177,58 +215,34 @@ __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
 template <int CPL, int R, typename ScaleT>
 __global__ __launch_bounds__(256) void mlp_gate_up_kernel(QhMlpParams p) {
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
   u32x4 xr[CPL];
   load_x_slice<CPL>(xr, p.x, p.x2, p.norm_w, p.eps, K, lane);
   const int ngroups = (p.N + R - 1) / R;
-  const ScaleT* sg = (const ScaleT*)p.sg;
-  const ScaleT* su = (const ScaleT*)p.su;
 
   for (int g = blockIdx.x * 4 + wid; g < ngroups; g += gridDim.x * 4) {
     const int row0 = g * R;
     u32x2 wg[R][CPL], wu[R][CPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, p.N - 1);
-      const uint8_t* gr = p.wg + (size_t)row * K;
-      const uint8_t* ur = p.wu + (size_t)row * K;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        const bool ok = c * 8 < K;
-        wg[r][j] = ok ? ld_w8(gr + c * 8) : u32x2{0u, 0u};
-        wu[r][j] = ok ? ld_w8(ur + c * 8) : u32x2{0u, 0u};
-      }
-    }
+    float sg[R][CPL], su[R][CPL];
+    load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, row0, K, lane);
+    load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, row0, K, lane);
     float ag[R], au[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) { ag[r] = 0.0f; au[r] = 0.0f; }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, p.N - 1);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        if (c * 8 < K) {
-          const int si = scale_index(p.kb, row, c >> 4);
-          const float scg = load_scale<ScaleT>(sg, si);
-          const float scu = load_scale<ScaleT>(su, si);
-          ag[r] = fmaf(dot8_e4m3_bf16(wg[r][j].x, wg[r][j].y, xr[j], 0.0f), scg, ag[r]);
-          au[r] = fmaf(dot8_e4m3_bf16(wu[r][j].x, wu[r][j].y, xr[j], 0.0f), scu, au[r]);
-        }
-      }
-    }
+    dot_rows<CPL, R>(ag, wg, sg, xr);
+    dot_rows<CPL, R>(au, wu, su, xr);
 #pragma unroll
     for (int r = 0; r < R; ++r) { ag[r] = wave_sum(ag[r]); au[r] = wave_sum(au[r]); }
-    const float gv = pick_lane<R>(ag, lane);
-    const float uv = pick_lane<R>(au, lane);
-    const int row = row0 + lane;
-    if (lane < R && row < p.N) {
-      // SiLU on the fp32 accumulators (fused_kernels.cu:476).
-      p.m_out[row] = f2bf(qh_silu(gv) * uv);
-      if (p.g_out) p.g_out[row] = f2bf(gv);
-      if (p.u_out) p.u_out[row] = f2bf(uv);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int row = row0 + r;
+        if (row < p.N) {
+          // SiLU on the fp32 accumulators (fused_kernels.cu:476).
+          p.m_out[row] = f2bf(qh_silu(ag[r]) * au[r]);
+          if (p.g_out) p.g_out[row] = f2bf(ag[r]);
+          if (p.u_out) p.u_out[row] = f2bf(au[r]);
+        }
+      }
     }
   }
 }
@@ -248,7 +262,7 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float v2, int i2) {
 template <int CPL, int R>
 __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
   u32x4 xr[CPL];
   load_x_slice<CPL>(xr, p.x, nullptr, p.norm_w, p.eps, K, lane);
@@ -266,7 +280,8 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
-        wr[r][j] = (c * 8 < K) ? ld_w16(wrow + c * 8) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = ld_w16(wrow + (c * 8 < K ? c : 0) * 8);
+        wr[r][j] = (c * 8 < K) ? v : u32x4{0u, 0u, 0u, 0u};
       }
     }
     float acc[R];
@@ -298,22 +313,13 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
     float v = s_v[0];
     int i = s_i[0];
     for (int w = 1; w < 4; ++w) amax_merge(v, i, s_v[w], s_i[w]);
-    p.part_val[blockIdx.x] = v;
-    p.part_idx[blockIdx.x] = i;
-    __threadfence();
-    const unsigned prev = atomicAdd(p.counter, 1u);
-    s_last = (prev == gridDim.x - 1);
+    pub_store(&p.part_val[blockIdx.x], v);
+    pub_store(&p.part_idx[blockIdx.x], i);
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(p.counter, gridDim.x, &s_last)) return;
   float v = -INFINITY;
   int i = 0x7fffffff;
-  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) {
-    const float bv = __hip_atomic_load(&p.part_val[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int bi = __hip_atomic_load(&p.part_idx[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    amax_merge(v, i, bv, bi);
-  }
+  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) amax_merge(v, i, pub_load(&p.part_val[b]), pub_load(&p.part_idx[b]));
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float v2 = __shfl_xor(v, o, 64);
@@ -335,7 +341,7 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
       if (p.tok_hist && t >= 0 && t < p.hist_len) p.tok_hist[t] = (int64_t)fi;
       p.pos[0] = t + 1;
     }
-    __hip_atomic_store(p.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    reset_counter(p.counter);
   }
   __syncthreads();
   if (p.embed) {

@@ -105,6 +105,44 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
   return red[0] + red[1] + red[2] + red[3];
 }
 
+// ---- cross-workgroup hand-off ---------------------------------------------
+// A kernel's workgroups publish partial results to the last one to finish.
+// __threadfence() would write back and invalidate the whole L2 of the XCD
+// (buffer_wbl2 / buffer_inv) in every workgroup.  Instead the published values
+// are device-scope atomic stores and loads (coherent across XCDs without any
+// cache maintenance); the publisher waits for its stores to complete before
+// it increments the arrival counter, so the last arriver reads them all.
+__device__ __forceinline__ void pub_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_store(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float pub_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int pub_load(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's outstanding memory operations have completed.
+__device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Called by every thread of the block after it published its values: returns
+// true in the last block to arrive.  The counter returns to zero for the next
+// launch (the last block resets it).
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned n_blocks, int* s_flag) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = prev == n_blocks - 1;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+__device__ __forceinline__ void reset_counter(unsigned* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- math --------------------------------------------------------------------
 __device__ __forceinline__ float qh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float qh_silu(float x) { return x / (1.0f + __expf(-x)); }

@@ -15,7 +15,7 @@ struct QhGdnParams {
   const float* dt_bias;     // [Hv]
   const uint16_t* norm_w;   // [dv] bf16 (plain weight)
   float* state;             // [Hv, dk, dv] fp32, updated in place
-  uint16_t* core;           // [Hv * dv] bf16 scratch (delta-rule output)
+  float* core;              // [Hv * dv] fp32 scratch: bf16-rounded delta-rule output
   uint16_t* out;            // [Hv * dv] bf16 gated output
   unsigned* counters;       // [Hv] zero-initialised arrival counters
   const int* pos_dev;       // optional device position t

@@ -63,7 +63,7 @@ class Qwen35FP8Engine:
         self.a = torch.zeros(cfg.linear_num_value_heads, **bf)
         self.b = torch.zeros(cfg.linear_num_value_heads, **bf)
         self.mix_out = torch.zeros(max(cfg.attn_out_dim, cfg.value_dim), **bf)
-        self.core = torch.zeros(cfg.value_dim, **bf)
+        self.core = torch.zeros(cfg.value_dim, dtype=torch.float32, device=dev)
         self.m = torch.zeros(I, **bf)
         self.logits = torch.zeros(V, **bf)
         self.tok = torch.zeros(1, 1, dtype=torch.int64, device=dev)

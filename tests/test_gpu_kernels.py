@@ -24,6 +24,7 @@ _KEEP = []
 
 @pytest.fixture(autouse=True)
 def _keep_alive():
+    abi.load().qh_clear_error()   # the error string is per thread and persists
     yield
     torch.cuda.synchronize()
     _KEEP.clear()
@@ -347,7 +348,7 @@ def test_gdn_decode(t):
     lib = abi.load()
     ring = cu(bf(_ring_from_ordered(d["conv_state"].float(), t)))
     Sg = cu(d["S"])
-    coreg = torch.empty(Hv * dv, dtype=torch.bfloat16, device=DEV)
+    coreg = torch.empty(Hv * dv, dtype=torch.float32, device=DEV)
     out = torch.empty(Hv * dv, dtype=torch.bfloat16, device=DEV)
     counters = torch.zeros(Hv, dtype=torch.int32, device=DEV)
     abi.check(lib.qh_gdn_decode(abi.ptr(cu(d["mixed"])), abi.ptr(cu(d["a"])), abi.ptr(cu(d["b"])),
