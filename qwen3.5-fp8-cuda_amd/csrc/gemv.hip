@@ -57,49 +57,60 @@ __device__ __forceinline__ u32x4 norm_bf16x8(u32x4 a, float rms, f32x4 w0, f32x4
   return r;
 }
 
-// Loads this lane's activation slice (chunks lane + 64*j) and applies the
-// optional add / RMSNorm prologue.  Chunks past K read as zero.  Every load is
-// issued unconditionally from a clamped address, so they are all in flight at
-// once (no per-chunk branch, no per-chunk wait).
+// Activation prologue, once per workgroup: x (optionally + x2, rounded to
+// bf16) and the optional (1+w) RMSNorm are built cooperatively into LDS
+// (sx, K bf16), then every wave copies its slice (chunks lane + 64*j, zero
+// past K) into registers.  Callers issue their first row group's weight loads
+// before calling this, so the weight stream overlaps the prologue.
 template <int CPL>
-__device__ __forceinline__ void load_x_slice(u32x4 (&xr)[CPL], const uint16_t* x,
-                                             const uint16_t* x2, const float* norm_w,
-                                             float eps, int K, int lane) {
-  bool ok[CPL];
+__device__ __forceinline__ void block_x_prologue(u32x4 (&xr)[CPL], uint16_t* sx, float* red,
+                                                 const uint16_t* x, const uint16_t* x2,
+                                                 const float* norm_w, float eps, int K) {
+  constexpr int MAXC = (CPL * 64 + 255) / 256;  // 8-element chunks per thread
+  const int tid = threadIdx.x;
+  const int nch = K / 8;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  u32x4 v[MAXC];
+  f32x4 w0[MAXC], w1[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = tid + 256 * i;
+    const int cc = c < nch ? c : 0;
+    v[i] = *(const u32x4*)(x + cc * 8);
+    if (norm_w) {
+      w0[i] = *(const f32x4*)(norm_w + cc * 8);
+      w1[i] = *(const f32x4*)(norm_w + cc * 8 + 4);
+    }
+  }
+  if (x2) {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const int c = tid + 256 * i;
+      v[i] = add_bf16x8(v[i], *(const u32x4*)(x2 + (c < nch ? c : 0) * 8));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) v[i] = tid + 256 * i < nch ? v[i] : zero;
+  if (norm_w) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
+    ss = block_sum_256(ss, red);
+    const float rms = rsqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) v[i] = norm_bf16x8(v[i], rms, w0[i], w1[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = tid + 256 * i;
+    if (c < nch) *(u32x4*)(sx + c * 8) = v[i];
+  }
+  __syncthreads();
+  const int lane = tid & 63;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + 64 * j;
-    ok[j] = c * 8 < K;
-    xr[j] = *(const u32x4*)(x + (ok[j] ? c : 0) * 8);
-  }
-  if (x2) {
-    u32x4 b[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) b[j] = *(const u32x4*)(x2 + (ok[j] ? lane + 64 * j : 0) * 8);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) xr[j] = add_bf16x8(xr[j], b[j]);
-  }
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) xr[j] = ok[j] ? xr[j] : zero;
-  if (norm_w) {
-    f32x4 w0[CPL], w1[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const float* wp = norm_w + (ok[j] ? lane + 64 * j : 0) * 8;
-      w0[j] = *(const f32x4*)wp;
-      w1[j] = *(const f32x4*)(wp + 4);
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) ss = sumsq_bf16x8(xr[j], ss);
-    ss = wave_sum(ss);
-    const float rms = rsqrtf(ss / (float)K + eps);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const u32x4 n = norm_bf16x8(xr[j], rms, w0[j], w1[j]);
-      xr[j] = ok[j] ? n : zero;
-    }
+    xr[j] = c < nch ? *(const u32x4*)(sx + c * 8) : zero;
   }
 }
 
@@ -169,28 +180,38 @@ __device__ __forceinline__ void dot_rows(float (&acc)[R], const u32x2 (&wr)[R][C
 
 template <int CPL, int R, typename ScaleT>
 __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
+  __shared__ __align__(16) uint16_t sx[CPL * 512];
+  __shared__ float red[4];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
-  u32x4 xr[CPL];
-  load_x_slice<CPL>(xr, p.x, p.x2, p.norm_w, p.eps, K, lane);
+  const int stride = gridDim.x * 4;
+  int g = blockIdx.x * 4 + wid;
 
-  for (int g = blockIdx.x * 4 + wid; g < p.gtotal; g += gridDim.x * 4) {
+  auto seg_of = [&](int gg, QhGemvSeg& sg) {
     int si = 0;
 #pragma unroll
     for (int t = 1; t < 4; ++t)
-      if (t < p.nseg && g >= p.gstart[t]) si = t;
-    const QhGemvSeg sg = p.seg[si];
-    const int row0 = (g - p.gstart[si]) * R;
-
-    u32x2 wr[R][CPL];
-    float sc[R][CPL];
+      if (t < p.nseg && gg >= p.gstart[t]) si = t;
+    sg = p.seg[si];
+    return (gg - p.gstart[si]) * R;
+  };
+  u32x2 wr[R][CPL];
+  float sc[R][CPL];
+  QhGemvSeg sg;
+  int row0 = 0;
+  if (g < p.gtotal) {
+    row0 = seg_of(g, sg);
     load_rows<CPL, R, ScaleT>(wr, sc, sg.w, (const ScaleT*)sg.s, sg.kb, sg.n, row0, K, lane);
+  }
+  u32x4 xr[CPL];
+  block_x_prologue<CPL>(xr, sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+
+  while (g < p.gtotal) {
     float acc[R];
     dot_rows<CPL, R>(acc, wr, sc, xr);
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-
     // Every lane holds every row total after the butterfly; lane 0 stores
     // them with static indices (a lane-indexed pick would be lowered to a
     // dynamically indexed array spilled through LDS).
@@ -209,24 +230,35 @@ __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
         }
       }
     }
+    g += stride;
+    if (g < p.gtotal) {
+      row0 = seg_of(g, sg);
+      load_rows<CPL, R, ScaleT>(wr, sc, sg.w, (const ScaleT*)sg.s, sg.kb, sg.n, row0, K, lane);
+    }
   }
 }
 
 template <int CPL, int R, typename ScaleT>
 __global__ __launch_bounds__(256) void mlp_gate_up_kernel(QhMlpParams p) {
+  __shared__ __align__(16) uint16_t sx[CPL * 512];
+  __shared__ float red[4];
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
-  u32x4 xr[CPL];
-  load_x_slice<CPL>(xr, p.x, p.x2, p.norm_w, p.eps, K, lane);
   const int ngroups = (p.N + R - 1) / R;
+  const int stride = gridDim.x * 4;
+  int g = blockIdx.x * 4 + wid;
+  u32x2 wg[R][CPL], wu[R][CPL];
+  float sg[R][CPL], su[R][CPL];
+  if (g < ngroups) {
+    load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, g * R, K, lane);
+    load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, g * R, K, lane);
+  }
+  u32x4 xr[CPL];
+  block_x_prologue<CPL>(xr, sx, red, p.x, p.x2, p.norm_w, p.eps, K);
 
-  for (int g = blockIdx.x * 4 + wid; g < ngroups; g += gridDim.x * 4) {
+  while (g < ngroups) {
     const int row0 = g * R;
-    u32x2 wg[R][CPL], wu[R][CPL];
-    float sg[R][CPL], su[R][CPL];
-    load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, row0, K, lane);
-    load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, row0, K, lane);
     float ag[R], au[R];
     dot_rows<CPL, R>(ag, wg, sg, xr);
     dot_rows<CPL, R>(au, wu, su, xr);
@@ -244,6 +276,11 @@ __global__ __launch_bounds__(256) void mlp_gate_up_kernel(QhMlpParams p) {
         }
       }
     }
+    g += stride;
+    if (g < ngroups) {
+      load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, g * R, K, lane);
+      load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, g * R, K, lane);
+    }
   }
 }
 
@@ -260,36 +297,51 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float v2, int i2) {
 }
 
 template <int CPL, int R>
+__device__ __forceinline__ void load_bf16_rows(u32x4 (&wr)[R][CPL], const uint16_t* w, int N,
+                                               int row0, int K, int lane) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, N - 1);
+    const uint16_t* wrow = w + (size_t)row * K;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + 64 * j;
+      wr[r][j] = ld_w16(wrow + (c * 8 < K ? c : 0) * 8);
+    }
+  }
+}
+
+// Grid-stride over row groups with the next group's weights in flight while
+// the current one is reduced (two register buffers).
+template <int CPL, int R>
 __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
-  u32x4 xr[CPL];
-  load_x_slice<CPL>(xr, p.x, nullptr, p.norm_w, p.eps, K, lane);
   const int ngroups = (p.N + R - 1) / R;
+  const int stride = gridDim.x * 4;
   float best_v = -INFINITY;
   int best_i = 0x7fffffff;
 
-  for (int g = blockIdx.x * 4 + wid; g < ngroups; g += gridDim.x * 4) {
+  __shared__ __align__(16) uint16_t sx[CPL * 512];
+  __shared__ float red[4];
+  int g = blockIdx.x * 4 + wid;
+  u32x4 wa[R][CPL];
+  if (g < ngroups) load_bf16_rows<CPL, R>(wa, p.w, p.N, g * R, K, lane);
+  u32x4 xr[CPL];
+  block_x_prologue<CPL>(xr, sx, red, p.x, nullptr, p.norm_w, p.eps, K);
+
+  while (g < ngroups) {
+    const int gn = g + stride;
+    u32x4 wb[R][CPL];
+    if (gn < ngroups) load_bf16_rows<CPL, R>(wb, p.w, p.N, gn * R, K, lane);
     const int row0 = g * R;
-    u32x4 wr[R][CPL];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, p.N - 1);
-      const uint16_t* wrow = p.w + (size_t)row * K;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        const u32x4 v = ld_w16(wrow + (c * 8 < K ? c : 0) * 8);
-        wr[r][j] = (c * 8 < K) ? v : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       acc[r] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[r] = dot8_bf16(wr[r][j], xr[j], acc[r]);
+      for (int j = 0; j < CPL; ++j) acc[r] = dot8_bf16(wa[r][j], xr[j], acc[r]);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
@@ -302,6 +354,11 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
         if (p.logits && lane == r) p.logits[row] = f2bf(acc[r]);
       }
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) wa[r][j] = wb[r][j];
+    g = gn;
   }
 
   __shared__ float s_v[4];
@@ -433,7 +490,7 @@ int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st) {
 
 int qh_lm_head_grid(int N) {
   const int ng = (N + 3) / 4;
-  return std::max(1, std::min(1024, (ng + 3) / 4));
+  return std::max(1, std::min(512, (ng + 3) / 4));
 }
 
 int qh_launch_lm_head(QhLmHeadParams p, int grid, hipStream_t st) {
