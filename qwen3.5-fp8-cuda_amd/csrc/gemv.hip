@@ -20,12 +20,11 @@
 #include "qh_kernels.h"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 
 namespace {
 
-__device__ __forceinline__ u32x2 ld_w8(const uint8_t* p) {
-  return __builtin_nontemporal_load((const u32x2*)p);
-}
 __device__ __forceinline__ u32x4 ld_w16(const uint16_t* p) {
   return __builtin_nontemporal_load((const u32x4*)p);
 }
@@ -60,8 +59,139 @@ __device__ __forceinline__ u32x4 norm_bf16x8(u32x4 a, float rms, f32x4 w0, f32x4
 // Activation prologue, once per workgroup: x (optionally + x2, rounded to
 // bf16) and the optional (1+w) RMSNorm are built cooperatively into LDS
 // (sx, K bf16), then every wave copies its slice (chunks lane + 64*j, zero
-// past K) into registers.  Callers issue their first row group's weight loads
-// before calling this, so the weight stream overlaps the prologue.
+// past K) into registers.  Split in two: XIn's loads are issued first, then
+// the caller issues its weight pipeline, then block_x_finish consumes XIn.
+// Vector-memory counters complete in order, so loads issued after the weight
+// stream would make the prologue wait for every weight load ahead of them.
+template <int CPL>
+struct XIn {
+  static constexpr int MAXC = (CPL * 64 + 255) / 256;  // 8-element chunks per thread
+  u32x4 v[MAXC], v2[MAXC];
+  f32x4 w0[MAXC], w1[MAXC];
+};
+
+// Large K (CPL > 8, one row group in flight per wave): the activation loads are
+// issued after the weights instead, so they hold no registers while the weight
+// stream is issued; the first group's weights are needed before any compute
+// anyway.
+template <int CPL>
+constexpr bool early_x() { return CPL <= 8; }
+
+template <int CPL>
+__device__ __forceinline__ void block_x_load(XIn<CPL>& in, const uint16_t* x, const uint16_t* x2,
+                                             const float* norm_w, int K) {
+  const int tid = threadIdx.x;
+  const int nch = K / 8;
+#pragma unroll
+  for (int i = 0; i < XIn<CPL>::MAXC; ++i) {
+    const int c = tid + 256 * i;
+    const int cc = c < nch ? c : 0;
+    in.v[i] = *(const u32x4*)(x + cc * 8);
+    if (x2) in.v2[i] = *(const u32x4*)(x2 + cc * 8);
+    if (norm_w) {
+      in.w0[i] = *(const f32x4*)(norm_w + cc * 8);
+      in.w1[i] = *(const f32x4*)(norm_w + cc * 8 + 4);
+    }
+  }
+}
+
+// Builds the (normalised) activation in LDS; returns after the barrier.
+template <int CPL>
+__device__ __forceinline__ void block_x_finish(XIn<CPL>& in, uint16_t* sx, float* red, bool has_x2,
+                                               bool has_norm, float eps, int K) {
+  constexpr int MAXC = XIn<CPL>::MAXC;
+  const int tid = threadIdx.x;
+  const int nch = K / 8;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  u32x4 v[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    v[i] = has_x2 ? add_bf16x8(in.v[i], in.v2[i]) : in.v[i];
+    v[i] = tid + 256 * i < nch ? v[i] : zero;
+  }
+  if (has_norm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
+    ss = block_sum_256(ss, red);
+    const float rms = rsqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) v[i] = norm_bf16x8(v[i], rms, in.w0[i], in.w1[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = tid + 256 * i;
+    if (c < nch) *(u32x4*)(sx + c * 8) = v[i];
+  }
+  __syncthreads();
+}
+
+// Prologue variant for large K: loads and combines x / x2 in one pass and
+// fetches the norm weights only after the sum of squares, so at most MAXC
+// chunks are live while a wave's weight loads are in flight.
+template <int CPL>
+__device__ __forceinline__ void block_x_direct(uint16_t* sx, float* red, const uint16_t* x,
+                                               const uint16_t* x2, const float* norm_w, float eps,
+                                               int K) {
+  constexpr int MAXC = XIn<CPL>::MAXC;
+  const int tid = threadIdx.x;
+  const int nch = K / 8;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  u32x4 v[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = tid + 256 * i;
+    const int cc = c < nch ? c : 0;
+    u32x4 a = *(const u32x4*)(x + cc * 8);
+    if (x2) a = add_bf16x8(a, *(const u32x4*)(x2 + cc * 8));
+    v[i] = c < nch ? a : zero;
+  }
+  if (norm_w) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
+    ss = block_sum_256(ss, red);
+    const float rms = rsqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const int cc = tid + 256 * i < nch ? tid + 256 * i : 0;
+      v[i] = norm_bf16x8(v[i], rms, *(const f32x4*)(norm_w + cc * 8),
+                         *(const f32x4*)(norm_w + cc * 8 + 4));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = tid + 256 * i;
+    if (c < nch) *(u32x4*)(sx + c * 8) = v[i];
+  }
+  __syncthreads();
+}
+
+// The lane's activation slice: chunk j holds x[8c .. 8c+8), c = lane + 64 j,
+// zero past K.  XLDS (large K): chunks are read from LDS at every use instead
+// of occupying 4*CPL registers for the kernel's lifetime.
+template <int CPL, bool XLDS>
+struct XSlice {
+  u32x4 r[XLDS ? 1 : CPL];
+  const uint16_t* sx;
+  int nch, lane;
+  __device__ __forceinline__ void init(const uint16_t* sx_, int K) {
+    sx = sx_;
+    nch = K / 8;
+    lane = threadIdx.x & 63;
+    if (!XLDS) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) r[XLDS ? 0 : j] = get_lds(j);
+    }
+  }
+  __device__ __forceinline__ u32x4 get_lds(int j) const {
+    const int c = lane + 64 * j;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    return c < nch ? *(const u32x4*)(sx + c * 8) : zero;
+  }
+  __device__ __forceinline__ u32x4 operator[](int j) const { return XLDS ? get_lds(j) : r[XLDS ? 0 : j]; }
+};
+
 template <int CPL>
 __device__ __forceinline__ void block_x_prologue(u32x4 (&xr)[CPL], uint16_t* sx, float* red,
                                                  const uint16_t* x, const uint16_t* x2,
@@ -114,30 +244,68 @@ __device__ __forceinline__ void block_x_prologue(u32x4 (&xr)[CPL], uint16_t* sx,
   }
 }
 
-// Loads R rows of this lane's weight chunks (non-temporal) and the matching
-// fp32 scales; chunks past K get zero weights and a zero scale.
-template <int CPL, int R, typename ScaleT>
-__device__ __forceinline__ void load_rows(u32x2 (&wr)[R][CPL], float (&sc)[R][CPL],
-                                          const uint8_t* w, const ScaleT* s, int kb, int n,
-                                          int row0, int K, int lane) {
+// ---- buffer-resource loads ----------------------------------------------------
+// Weights and scales are read through buffer resources sized to their tensor:
+// a load at an offset past the range returns zero without touching memory.
+// Rows past n, chunks past K and pipeline slots past the last group all use
+// kOob, so every wave issues the same instruction stream (the compiler's
+// in-order vmcnt bookkeeping then stays exact across the software pipeline)
+// while only real bytes are fetched.  Tensors must be smaller than 2^31 bytes
+// (checked by the launchers) so that kOob plus any folded immediate offset stays
+// out of range.
+constexpr uint32_t kOob = 0x80000000u;
+typedef __amdgpu_buffer_rsrc_t qh_rsrc;
+
+__device__ __forceinline__ qh_rsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x2 bload_w8(qh_rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2 /* nt: streaming */);
+}
+__device__ __forceinline__ uint16_t bload_u16(qh_rsrc r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <typename ScaleT> __device__ __forceinline__ float bload_scale(qh_rsrc r, uint32_t i);
+template <> __device__ __forceinline__ float bload_scale<float>(qh_rsrc r, uint32_t i) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i == kOob ? kOob : i * 4u, 0, 0));
+}
+template <> __device__ __forceinline__ float bload_scale<uint16_t>(qh_rsrc r, uint32_t i) {
+  return bf2f(bload_u16(r, i == kOob ? kOob : i * 2u));
+}
+
+// Number of scale entries of an [n, K] matrix in scale mode kb (see scale_index).
+__host__ __device__ __forceinline__ uint32_t scale_count(int kb, int n) {
+  if (kb > 1) return (uint32_t)((n + 127) >> 7) * (uint32_t)kb;
+  if (kb == 1) return (uint32_t)n;
+  return (uint32_t)n * (uint32_t)(-kb);
+}
+
+// Issues the loads of R rows (row0 ..) of this lane's weight chunks and their
+// fp32 scales.  BLK: 128x128 block scales, which the R rows (R divides 128,
+// row0 a multiple of R) share, so one scale per chunk is loaded.  Rows past n,
+// chunks past K and !valid groups load zeros.
+template <int CPL, int R, bool BLK, typename ScaleT>
+__device__ __forceinline__ void issue_rows(u32x2 (&wr)[R][CPL], float (&sc)[R][CPL], qh_rsrc wrs,
+                                           qh_rsrc srs, int kb, int n, int row0, bool valid, int K,
+                                           int lane) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, n - 1);
-    const uint8_t* wrow = w + (size_t)row * K;
+    const int row = row0 + r;
+    const bool okr = valid && row < n;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
-      wr[r][j] = ld_w8(wrow + (c * 8 < K ? c : 0) * 8);
+      const bool ok = okr && c * 8 < K;
+      wr[r][j] = bload_w8(wrs, ok ? (uint32_t)row * (uint32_t)K + (uint32_t)c * 8u : kOob);
     }
   }
-  if (kb > 1) {
-    // 128x128 block scales: the R rows (R divides 128) share one row block.
-    const ScaleT* srow = s + (row0 >> 7) * kb;
+  if (BLK) {
     float b[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
-      b[j] = load_scale<ScaleT>(srow, c * 8 < K ? (c >> 4) : 0);
+      const bool ok = valid && row0 < n && c * 8 < K;
+      b[j] = bload_scale<ScaleT>(srs, ok ? (uint32_t)((row0 >> 7) * kb + (c >> 4)) : kOob);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -146,40 +314,44 @@ __device__ __forceinline__ void load_rows(u32x2 (&wr)[R][CPL], float (&sc)[R][CP
   } else {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int row = min(row0 + r, n - 1);
+      const int row = row0 + r;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
-        sc[r][j] = load_scale<ScaleT>(s, scale_index(kb, row, c * 8 < K ? (c >> 4) : 0));
+        const bool ok = valid && row < n && c * 8 < K;
+        sc[r][j] = bload_scale<ScaleT>(srs, ok ? (uint32_t)scale_index(kb, row, c >> 4) : kOob);
       }
     }
   }
-  const u32x2 z = {0u, 0u};
+}
+
+template <int CPL, int R, bool XLDS>
+__device__ __forceinline__ void dot_rows(float (&acc)[R], const u32x2 (&wr)[R][CPL],
+                                         const float (&sc)[R][CPL], const XSlice<CPL, XLDS>& xs) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const bool ok = (lane + 64 * j) * 8 < K;
+    const u32x4 xj = xs[j];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      wr[r][j] = ok ? wr[r][j] : z;
-      sc[r][j] = ok ? sc[r][j] : 0.0f;
-    }
+    for (int r = 0; r < R; ++r)
+      acc[r] = fmaf(dot8_e4m3_bf16(wr[r][j].x, wr[r][j].y, xj, 0.0f), sc[r][j], acc[r]);
   }
 }
 
-template <int CPL, int R>
-__device__ __forceinline__ void dot_rows(float (&acc)[R], const u32x2 (&wr)[R][CPL],
-                                         const float (&sc)[R][CPL], const u32x4 (&xr)[CPL]) {
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    acc[r] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-      acc[r] = fmaf(dot8_e4m3_bf16(wr[r][j].x, wr[r][j].y, xr[j], 0.0f), sc[r][j], acc[r]);
-  }
-}
+// Software pipeline shared by the E4M3 GEMV kernels: a wave walks the row
+// groups g0, g0 + stride, ... (stride = all waves of the grid) and keeps P
+// groups' loads in flight (slot i % P holds group i), so the weight stream of
+// a wave never waits a full memory round trip between groups.  The loop body
+// is unrolled over the P slots so every register array is indexed statically.
+// Minimum resident waves per SIMD asked of the compiler: decode GEMVs want every
+// row group of the grid in flight at once (2560 rows of a K=9216 projection need
+// three waves per SIMD on 256 CUs).
+constexpr int gemv_min_waves(int cpl) { return cpl <= 8 ? 4 : 3; }
 
-template <int CPL, int R, typename ScaleT>
-__global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
+template <int CPL, int R, int P, bool BLK, typename ScaleT>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void gemv_e4m3_kernel(QhGemvParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[4];
   const int lane = threadIdx.x & 63;
@@ -188,58 +360,82 @@ __global__ __launch_bounds__(256) void gemv_e4m3_kernel(QhGemvParams p) {
   const int stride = gridDim.x * 4;
   int g = blockIdx.x * 4 + wid;
 
-  auto seg_of = [&](int gg, QhGemvSeg& sg) {
+  u32x2 wr[P][R][CPL];
+  float sc[P][R][CPL];
+  float res[P][R];   // residual for lane r's row r (epilogue), prefetched with the slot
+  int srow0[P], sseg[P];
+
+  // Issues slot s = group gg's loads (zeros when gg is past the last group).
+  auto issue = [&](auto& w_, auto& s_, float (&res_)[R], int& row0_, int& seg_, int gg) {
     int si = 0;
 #pragma unroll
     for (int t = 1; t < 4; ++t)
       if (t < p.nseg && gg >= p.gstart[t]) si = t;
-    sg = p.seg[si];
-    return (gg - p.gstart[si]) * R;
-  };
-  u32x2 wr[R][CPL];
-  float sc[R][CPL];
-  QhGemvSeg sg;
-  int row0 = 0;
-  if (g < p.gtotal) {
-    row0 = seg_of(g, sg);
-    load_rows<CPL, R, ScaleT>(wr, sc, sg.w, (const ScaleT*)sg.s, sg.kb, sg.n, row0, K, lane);
-  }
-  u32x4 xr[CPL];
-  block_x_prologue<CPL>(xr, sx, red, p.x, p.x2, p.norm_w, p.eps, K);
-
-  while (g < p.gtotal) {
-    float acc[R];
-    dot_rows<CPL, R>(acc, wr, sc, xr);
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-    // Every lane holds every row total after the butterfly; lane 0 stores
-    // them with static indices (a lane-indexed pick would be lowered to a
-    // dynamically indexed array spilled through LDS).
-    if (lane == 0) {
+    const QhGemvSeg& sg = p.seg[si];
+    const bool valid = gg < p.gtotal;
+    row0_ = (gg - p.gstart[si]) * R;
+    seg_ = si;
+    const qh_rsrc wrs = make_rsrc(sg.w, (uint32_t)sg.n * (uint32_t)K);
+    const qh_rsrc srs = make_rsrc(sg.s, scale_count(sg.kb, sg.n) * (uint32_t)sizeof(ScaleT));
+    issue_rows<CPL, R, BLK, ScaleT>(w_, s_, wrs, srs, sg.kb, sg.n, row0_, valid, K, lane);
+    if (p.res1) {
+      const qh_rsrc r1 = make_rsrc(p.res1, (uint32_t)sg.n * 2u);
+      const qh_rsrc r2 = make_rsrc(p.res2, p.res2 ? (uint32_t)sg.n * 2u : 0u);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
-        if (row < sg.n) {
-          float y = rbf(acc[r]);
-          if (p.res1) {
-            float res = bf2f(p.res1[row]);
-            if (p.res2) res = rbf(res + bf2f(p.res2[row]));
-            y = res + y;
-          }
-          sg.y[row] = f2bf(y);
-        }
+        const int row = row0_ + r;
+        const uint32_t off = valid && row < sg.n ? (uint32_t)row * 2u : kOob;
+        float v = bf2f(bload_u16(r1, off));
+        if (p.res2) v = rbf(v + bf2f(bload_u16(r2, off)));
+        res_[r] = v;
       }
     }
-    g += stride;
-    if (g < p.gtotal) {
-      row0 = seg_of(g, sg);
-      load_rows<CPL, R, ScaleT>(wr, sc, sg.w, (const ScaleT*)sg.s, sg.kb, sg.n, row0, K, lane);
+  };
+  (void)res;
+
+  XIn<CPL> xin;
+  if (early_x<CPL>()) block_x_load<CPL>(xin, p.x, p.x2, p.norm_w, K);
+#pragma unroll
+  for (int s = 0; s < P; ++s) issue(wr[s], sc[s], res[s], srow0[s], sseg[s], g + s * stride);
+  if (early_x<CPL>())
+    block_x_finish<CPL>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  else
+    block_x_direct<CPL>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+  XSlice<CPL, (CPL > 8)> xs;
+  xs.init(sx, K);
+
+  for (;;) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      if (g >= p.gtotal) return;
+      float acc[R];
+      dot_rows<CPL, R>(acc, wr[s], sc[s], xs);
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+      // Every lane holds every row total after the butterfly; lane 0 stores
+      // them with static indices (a lane-indexed pick would be lowered to a
+      // dynamically indexed array spilled through LDS).
+      if (lane == 0) {
+        const QhGemvSeg& sg = p.seg[sseg[s]];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = srow0[s] + r;
+          if (row < sg.n) {
+            float y = rbf(acc[r]);
+            if (p.res1) y = res[s][r] + y;
+            sg.y[row] = f2bf(y);
+          }
+        }
+      }
+      issue(wr[s], sc[s], res[s], srow0[s], sseg[s], g + P * stride);
+      g += stride;
     }
   }
 }
 
-template <int CPL, int R, typename ScaleT>
-__global__ __launch_bounds__(256) void mlp_gate_up_kernel(QhMlpParams p) {
+template <int CPL, int R, int P, bool BLK, typename ScaleT>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void mlp_gate_up_kernel(QhMlpParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[4];
   const int lane = threadIdx.x & 63;
@@ -248,38 +444,201 @@ __global__ __launch_bounds__(256) void mlp_gate_up_kernel(QhMlpParams p) {
   const int ngroups = (p.N + R - 1) / R;
   const int stride = gridDim.x * 4;
   int g = blockIdx.x * 4 + wid;
-  u32x2 wg[R][CPL], wu[R][CPL];
-  float sg[R][CPL], su[R][CPL];
-  if (g < ngroups) {
-    load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, g * R, K, lane);
-    load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, g * R, K, lane);
-  }
-  u32x4 xr[CPL];
-  block_x_prologue<CPL>(xr, sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+  const qh_rsrc wgr = make_rsrc(p.wg, (uint32_t)p.N * (uint32_t)K);
+  const qh_rsrc wur = make_rsrc(p.wu, (uint32_t)p.N * (uint32_t)K);
+  const uint32_t sbytes = scale_count(p.kb, p.N) * (uint32_t)sizeof(ScaleT);
+  const qh_rsrc sgr = make_rsrc(p.sg, sbytes);
+  const qh_rsrc sur = make_rsrc(p.su, sbytes);
 
-  while (g < ngroups) {
-    const int row0 = g * R;
-    float ag[R], au[R];
-    dot_rows<CPL, R>(ag, wg, sg, xr);
-    dot_rows<CPL, R>(au, wu, su, xr);
+  XIn<CPL> xin;
+  if (early_x<CPL>()) block_x_load<CPL>(xin, p.x, p.x2, p.norm_w, K);
+  u32x2 wg[P][R][CPL], wu[P][R][CPL];
+  float sg[P][R][CPL], su[P][R][CPL];
 #pragma unroll
-    for (int r = 0; r < R; ++r) { ag[r] = wave_sum(ag[r]); au[r] = wave_sum(au[r]); }
-    if (lane == 0) {
+  for (int s = 0; s < P; ++s) {
+    const int gg = g + s * stride;
+    issue_rows<CPL, R, BLK, ScaleT>(wg[s], sg[s], wgr, sgr, p.kb, p.N, gg * R, gg < ngroups, K, lane);
+    issue_rows<CPL, R, BLK, ScaleT>(wu[s], su[s], wur, sur, p.kb, p.N, gg * R, gg < ngroups, K, lane);
+  }
+  if (early_x<CPL>())
+    block_x_finish<CPL>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  else
+    block_x_direct<CPL>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+  XSlice<CPL, (CPL > 8)> xs;
+  xs.init(sx, K);
+
+  for (;;) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
-        if (row < p.N) {
-          // SiLU on the fp32 accumulators (fused_kernels.cu:476).
-          p.m_out[row] = f2bf(qh_silu(ag[r]) * au[r]);
-          if (p.g_out) p.g_out[row] = f2bf(ag[r]);
-          if (p.u_out) p.u_out[row] = f2bf(au[r]);
+    for (int s = 0; s < P; ++s) {
+      if (g >= ngroups) return;
+      const int row0 = g * R;
+      float ag[R], au[R];
+      dot_rows<CPL, R>(ag, wg[s], sg[s], xs);
+      dot_rows<CPL, R>(au, wu[s], su[s], xs);
+#pragma unroll
+      for (int r = 0; r < R; ++r) { ag[r] = wave_sum(ag[r]); au[r] = wave_sum(au[r]); }
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = row0 + r;
+          if (row < p.N) {
+            // SiLU on the fp32 accumulators (fused_kernels.cu:476).
+            p.m_out[row] = f2bf(qh_silu(ag[r]) * au[r]);
+            if (p.g_out) p.g_out[row] = f2bf(ag[r]);
+            if (p.u_out) p.u_out[row] = f2bf(au[r]);
+          }
         }
       }
+      const int gn = g + P * stride;
+      issue_rows<CPL, R, BLK, ScaleT>(wg[s], sg[s], wgr, sgr, p.kb, p.N, gn * R, gn < ngroups, K, lane);
+      issue_rows<CPL, R, BLK, ScaleT>(wu[s], su[s], wur, sur, p.kb, p.N, gn * R, gn < ngroups, K, lane);
+      g += stride;
     }
-    g += stride;
-    if (g < ngroups) {
-      load_rows<CPL, R, ScaleT>(wg, sg, p.wg, (const ScaleT*)p.sg, p.kb, p.N, g * R, K, lane);
-      load_rows<CPL, R, ScaleT>(wu, su, p.wu, (const ScaleT*)p.su, p.kb, p.N, g * R, K, lane);
+  }
+}
+
+// ---- fast path: 128x128 block scales, K a multiple of 512 ---------------------
+// One row per wave and iteration.  Every row gets its own buffer resource
+// (base = the row, range = K bytes, or 0 when the slot has no row), so the
+// lane offsets are the constants lane*8 + 512*j and the per-row address math
+// is a few scalar instructions; the scales of the row's 128-row block come
+// the same way (lane l, chunk j reads k-block 4j + l/16).  Row totals are
+// reduced with DPP moves into a wave-uniform value.
+template <int CPL, typename ScaleT>
+__device__ __forceinline__ void issue_fast(u32x2 (&w)[CPL], float (&sc)[CPL], const uint8_t* W,
+                                           const void* S, int row, bool valid, uint32_t lw,
+                                           uint32_t ls) {
+  constexpr int K = CPL * 512, KB = K / 128;
+  const qh_rsrc wr = make_rsrc(W + (size_t)row * K, valid ? (uint32_t)K : 0u);
+  const qh_rsrc sr = make_rsrc((const ScaleT*)S + (size_t)(row >> 7) * KB,
+                               valid ? (uint32_t)(KB * sizeof(ScaleT)) : 0u);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) w[j] = bload_w8(wr, lw + 512u * j);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint32_t off = ls + (uint32_t)(4 * j * sizeof(ScaleT));
+    if (sizeof(ScaleT) == 4)
+      sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
+    else
+      sc[j] = bf2f(bload_u16(sr, off));
+  }
+}
+
+template <int CPL, bool XLDS>
+__device__ __forceinline__ float dot_row(const u32x2 (&w)[CPL], const float (&sc)[CPL],
+                                         const XSlice<CPL, XLDS>& xs) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) acc = fmaf(dot8_e4m3_bf16(w[j].x, w[j].y, xs[j], 0.0f), sc[j], acc);
+  return acc;
+}
+
+template <int CPL, int P, typename ScaleT>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void gemv_fast_kernel(QhGemvParams p) {
+  constexpr int K = CPL * 512;
+  __shared__ __align__(16) uint16_t sx[K];
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lw = lane * 8u, ls = (uint32_t)((lane >> 4) * sizeof(ScaleT));
+  const int stride = gridDim.x * 4;
+  int g = blockIdx.x * 4 + wid;
+
+  u32x2 w[P][CPL];
+  float sc[P][CPL];
+  float res[P];
+  int srow[P], sseg[P];
+  auto issue = [&](u32x2 (&w_)[CPL], float (&sc_)[CPL], float& res_, int& row_, int& seg_, int gg) {
+    int si = 0;
+#pragma unroll
+    for (int t = 1; t < 4; ++t)
+      if (t < p.nseg && gg >= p.gstart[t]) si = t;
+    const bool valid = gg < p.gtotal;
+    const int row = gg - p.gstart[si];
+    row_ = row;
+    seg_ = si;
+    issue_fast<CPL, ScaleT>(w_, sc_, p.seg[si].w, p.seg[si].s, row, valid, lw, ls);
+    if (p.res1) {
+      const qh_rsrc r1 = make_rsrc(p.res1 + row, valid ? 2u : 0u);
+      float v = bf2f(bload_u16(r1, 0));
+      if (p.res2) v = rbf(v + bf2f(bload_u16(make_rsrc(p.res2 + row, valid ? 2u : 0u), 0)));
+      res_ = v;
+    }
+  };
+
+  XIn<CPL> xin;
+  if (early_x<CPL>()) block_x_load<CPL>(xin, p.x, p.x2, p.norm_w, K);
+#pragma unroll
+  for (int s = 0; s < P; ++s) issue(w[s], sc[s], res[s], srow[s], sseg[s], g + s * stride);
+  if (early_x<CPL>())
+    block_x_finish<CPL>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  else
+    block_x_direct<CPL>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+  XSlice<CPL, (CPL > 8)> xs;
+  xs.init(sx, K);
+
+  for (;;) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      if (g >= p.gtotal) return;
+      const float acc = wave_total(dot_row<CPL>(w[s], sc[s], xs));
+      if (lane == 0) {
+        float y = rbf(acc);
+        if (p.res1) y = res[s] + y;
+        p.seg[sseg[s]].y[srow[s]] = f2bf(y);
+      }
+      issue(w[s], sc[s], res[s], srow[s], sseg[s], g + P * stride);
+      g += stride;
+    }
+  }
+}
+
+template <int CPL, int P, typename ScaleT>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void mlp_fast_kernel(QhMlpParams p) {
+  constexpr int K = CPL * 512;
+  __shared__ __align__(16) uint16_t sx[K];
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lw = lane * 8u, ls = (uint32_t)((lane >> 4) * sizeof(ScaleT));
+  const int stride = gridDim.x * 4;
+  int g = blockIdx.x * 4 + wid;
+
+  XIn<CPL> xin;
+  if (early_x<CPL>()) block_x_load<CPL>(xin, p.x, p.x2, p.norm_w, K);
+  u32x2 wg[P][CPL], wu[P][CPL];
+  float sg[P][CPL], su[P][CPL];
+#pragma unroll
+  for (int s = 0; s < P; ++s) {
+    const int gg = g + s * stride;
+    issue_fast<CPL, ScaleT>(wg[s], sg[s], p.wg, p.sg, gg, gg < p.N, lw, ls);
+    issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gg, gg < p.N, lw, ls);
+  }
+  if (early_x<CPL>())
+    block_x_finish<CPL>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  else
+    block_x_direct<CPL>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
+  XSlice<CPL, (CPL > 8)> xs;
+  xs.init(sx, K);
+
+  for (;;) {
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      if (g >= p.N) return;
+      const float ag = wave_total(dot_row<CPL>(wg[s], sg[s], xs));
+      const float au = wave_total(dot_row<CPL>(wu[s], su[s], xs));
+      if (lane == 0) {
+        // SiLU on the fp32 accumulators (fused_kernels.cu:476).
+        p.m_out[g] = f2bf(qh_silu(ag) * au);
+        if (p.g_out) p.g_out[g] = f2bf(ag);
+        if (p.u_out) p.u_out[g] = f2bf(au);
+      }
+      const int gn = g + P * stride;
+      issue_fast<CPL, ScaleT>(wg[s], sg[s], p.wg, p.sg, gn, gn < p.N, lw, ls);
+      issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gn, gn < p.N, lw, ls);
+      g += stride;
     }
   }
 }
@@ -408,20 +767,95 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
 }
 
 // ---- launchers ----------------------------------------------------------------
-constexpr int kMaxGrid = 4096;
+// Row-group size R and pipeline depth P per chunks-per-lane class (measured on
+// MI355X at the decode shapes: many waves with a few rows each, every wave of
+// the grid resident at once, two groups in flight per wave).
+// Generic kernels (any scale mode, any K % 8 == 0): one row, one group in
+// flight.  Fast kernels: two rows in flight per wave while the activation
+// slice lives in registers (K <= 4096), one above.
+constexpr int gemv_rows(int cpl) { return cpl > 0 ? 1 : 1; }
+constexpr int gemv_depth(int cpl) { return cpl > 0 ? 1 : 1; }
+constexpr int fast_depth(int cpl) { return cpl <= 6 ? 2 : 1; }
+constexpr uint32_t kMaxBufferBytes = 0x7fffffffu;
 
-template <int CPL, int R, typename ScaleT>
+int cu_count() {
+  static int cus[16] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Workgroups of `fn` (256 threads) that fit on the current device at once.
+int resident_blocks(const void* fn) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find({fn, dev});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 1;
+  const int n = per_cu * cus;
+  cache[{fn, dev}] = n;
+  return n;
+}
+
+template <int CPL, bool BLK, typename ScaleT>
 void launch_gemv_t(const QhGemvParams& p, hipStream_t st) {
-  const int grid = std::min(kMaxGrid, (p.gtotal + 3) / 4);
-  hipLaunchKernelGGL((gemv_e4m3_kernel<CPL, R, ScaleT>), dim3(grid), dim3(256), 0, st, p);
+  constexpr int R = gemv_rows(CPL), P = gemv_depth(CPL);
+  auto fn = gemv_e4m3_kernel<CPL, R, P, BLK, ScaleT>;
+  const int grid = std::max(1, std::min(resident_blocks((const void*)fn), (p.gtotal + 3) / 4));
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
 
-template <int CPL, int R, typename ScaleT>
+template <int CPL, bool BLK, typename ScaleT>
 void launch_mlp_t(const QhMlpParams& p, hipStream_t st) {
+  constexpr int R = gemv_rows(CPL), P = gemv_depth(CPL);
+  auto fn = mlp_gate_up_kernel<CPL, R, P, BLK, ScaleT>;
   const int ng = (p.N + R - 1) / R;
-  const int grid = std::min(kMaxGrid, (ng + 3) / 4);
-  hipLaunchKernelGGL((mlp_gate_up_kernel<CPL, R, ScaleT>), dim3(grid), dim3(256), 0, st, p);
+  const int grid = std::max(1, std::min(resident_blocks((const void*)fn), (ng + 3) / 4));
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
+
+template <int CPL, typename ScaleT>
+void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
+  // Two workgroups per CU, each wave walking several rows, measured faster than
+  // filling every slot (fewer activation prologues, same bytes in flight).
+  auto fn = gemv_fast_kernel<CPL, fast_depth(CPL), ScaleT>;
+  const int grid = std::max(1, std::min({resident_blocks((const void*)fn), 2 * cu_count(), (p.gtotal + 3) / 4}));
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
+}
+
+template <int CPL, typename ScaleT>
+void launch_mlp_fast_t(const QhMlpParams& p, hipStream_t st) {
+  auto fn = mlp_fast_kernel<CPL, fast_depth(CPL), ScaleT>;
+  const int grid = std::max(1, std::min({resident_blocks((const void*)fn), 2 * cu_count(), (p.N + 3) / 4}));
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
+}
+
+// Fast-path K values (K = 512 * CPL); other K use the generic kernels.
+#define QH_FAST_DISPATCH(CPL_VAL, CALL) \
+  switch (CPL_VAL) {                    \
+    case 2: CALL(2); return 0;          \
+    case 4: CALL(4); return 0;          \
+    case 5: CALL(5); return 0;          \
+    case 6: CALL(6); return 0;          \
+    case 8: CALL(8); return 0;          \
+    case 10: CALL(10); return 0;        \
+    case 12: CALL(12); return 0;        \
+    case 16: CALL(16); return 0;        \
+    case 18: CALL(18); return 0;        \
+    default: break;                     \
+  }
 
 // Smallest supported chunks-per-lane >= ceil(K / 512); 0 when K is too large.
 int pick_cpl(int K) {
@@ -432,23 +866,23 @@ int pick_cpl(int K) {
   return 0;
 }
 
-#define QH_CPL_DISPATCH(CPL_VAL, CALL4, CALL2) \
-  switch (CPL_VAL) {                           \
-    case 1: CALL4(1); break;                   \
-    case 2: CALL4(2); break;                   \
-    case 3: CALL4(3); break;                   \
-    case 4: CALL4(4); break;                   \
-    case 5: CALL4(5); break;                   \
-    case 6: CALL4(6); break;                   \
-    case 8: CALL4(8); break;                   \
-    case 10: CALL2(10); break;                 \
-    case 12: CALL2(12); break;                 \
-    case 16: CALL2(16); break;                 \
-    case 18: CALL2(18); break;                 \
-    case 20: CALL2(20); break;                 \
-    case 24: CALL2(24); break;                 \
-    case 32: CALL2(32); break;                 \
-    default: return -1;                        \
+#define QH_CPL_DISPATCH(CPL_VAL, CALL) \
+  switch (CPL_VAL) {                     \
+    case 1: CALL(1); break;              \
+    case 2: CALL(2); break;              \
+    case 3: CALL(3); break;              \
+    case 4: CALL(4); break;              \
+    case 5: CALL(5); break;              \
+    case 6: CALL(6); break;              \
+    case 8: CALL(8); break;              \
+    case 10: CALL(10); break;            \
+    case 12: CALL(12); break;            \
+    case 16: CALL(16); break;            \
+    case 18: CALL(18); break;            \
+    case 20: CALL(20); break;            \
+    case 24: CALL(24); break;            \
+    case 32: CALL(32); break;            \
+    default: return -1;                  \
   }
 
 }  // namespace
@@ -459,17 +893,37 @@ int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st) {
     qh_set_error("gemv: K=%d exceeds the supported maximum (16384)", p.K);
     return -1;
   }
-  const int R = cpl <= 8 ? 4 : 2;
+  constexpr int R = 1;
+  static_assert(gemv_rows(1) == R && gemv_rows(32) == R, "group size must not depend on CPL");
+  bool blk = true;
   p.gstart[0] = 0;
-  for (int i = 0; i < p.nseg; ++i) p.gstart[i + 1] = p.gstart[i] + (p.seg[i].n + R - 1) / R;
+  for (int i = 0; i < p.nseg; ++i) {
+    const QhGemvSeg& sg = p.seg[i];
+    const uint32_t sbytes = scale_count(sg.kb, sg.n) * (scale_bf16 ? 2u : 4u);
+    if ((uint64_t)sg.n * (uint64_t)p.K > kMaxBufferBytes || sbytes > kMaxBufferBytes) {
+      qh_set_error("gemv: segment %d (%d x %d) exceeds 2^31 bytes", i, sg.n, p.K);
+      return -1;
+    }
+    blk = blk && sg.kb > 1;
+    p.gstart[i + 1] = p.gstart[i] + (sg.n + R - 1) / R;
+  }
   for (int i = p.nseg + 1; i < 5; ++i) p.gstart[i] = p.gstart[p.nseg];
   p.gtotal = p.gstart[p.nseg];
   if (p.gtotal == 0) return 0;
-#define G4(C) (scale_bf16 ? launch_gemv_t<C, 4, uint16_t>(p, st) : launch_gemv_t<C, 4, float>(p, st))
-#define G2(C) (scale_bf16 ? launch_gemv_t<C, 2, uint16_t>(p, st) : launch_gemv_t<C, 2, float>(p, st))
-  QH_CPL_DISPATCH(cpl, G4, G2)
-#undef G4
-#undef G2
+  bool fast = p.K % 512 == 0;
+  for (int i = 0; i < p.nseg; ++i) fast = fast && p.seg[i].kb == p.K / 128;
+  if (fast) {
+#define F(C) (scale_bf16 ? launch_gemv_fast_t<C, uint16_t>(p, st) : launch_gemv_fast_t<C, float>(p, st))
+    QH_FAST_DISPATCH(p.K / 512, F)
+#undef F
+  }
+#define G(C)                                                              \
+  (blk ? (scale_bf16 ? launch_gemv_t<C, true, uint16_t>(p, st)             \
+                     : launch_gemv_t<C, true, float>(p, st))               \
+       : (scale_bf16 ? launch_gemv_t<C, false, uint16_t>(p, st)            \
+                     : launch_gemv_t<C, false, float>(p, st)))
+  QH_CPL_DISPATCH(cpl, G)
+#undef G
   return 0;
 }
 
@@ -480,11 +934,23 @@ int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st) {
     return -1;
   }
   if (p.N <= 0) return 0;
-#define M4(C) (scale_bf16 ? launch_mlp_t<C, 4, uint16_t>(p, st) : launch_mlp_t<C, 4, float>(p, st))
-#define M2(C) (scale_bf16 ? launch_mlp_t<C, 2, uint16_t>(p, st) : launch_mlp_t<C, 2, float>(p, st))
-  QH_CPL_DISPATCH(cpl, M4, M2)
-#undef M4
-#undef M2
+  if ((uint64_t)p.N * (uint64_t)p.K > kMaxBufferBytes) {
+    qh_set_error("mlp: %d x %d exceeds 2^31 bytes", p.N, p.K);
+    return -1;
+  }
+  if (p.K % 512 == 0 && p.kb == p.K / 128) {
+#define F(C) (scale_bf16 ? launch_mlp_fast_t<C, uint16_t>(p, st) : launch_mlp_fast_t<C, float>(p, st))
+    QH_FAST_DISPATCH(p.K / 512, F)
+#undef F
+  }
+  const bool blk = p.kb > 1;
+#define M(C)                                                              \
+  (blk ? (scale_bf16 ? launch_mlp_t<C, true, uint16_t>(p, st)              \
+                     : launch_mlp_t<C, true, float>(p, st))                \
+       : (scale_bf16 ? launch_mlp_t<C, false, uint16_t>(p, st)             \
+                     : launch_mlp_t<C, false, float>(p, st)))
+  QH_CPL_DISPATCH(cpl, M)
+#undef M
   return 0;
 }
 
@@ -499,10 +965,8 @@ int qh_launch_lm_head(QhLmHeadParams p, int grid, hipStream_t st) {
     qh_set_error("lm_head: K=%d unsupported (need K <= 4096)", p.K);
     return -1;
   }
-#define L4(C) hipLaunchKernelGGL((lm_head_argmax_kernel<C, 4>), dim3(grid), dim3(256), 0, st, p)
-#define L2(C) (void)0
-  QH_CPL_DISPATCH(cpl, L4, L2)
-#undef L4
-#undef L2
+#define L(C) hipLaunchKernelGGL((lm_head_argmax_kernel<(C <= 8 ? C : 8), 4>), dim3(grid), dim3(256), 0, st, p)
+  QH_CPL_DISPATCH(cpl, L)
+#undef L
   return 0;
 }

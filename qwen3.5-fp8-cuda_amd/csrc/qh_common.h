@@ -82,6 +82,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, QH_WAVE);
   return v;
 }
+// Sum of the 64 lanes' values as a wave-uniform result, with DPP moves only
+// (no LDS traffic): pairs (quad_perm xor 1, xor 2), then row_half_mirror and
+// row_mirror give every lane its 16-lane row sum, then row_bcast:15 and
+// row_bcast:31 fold the four rows into lane 63, which is read back.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_src(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_total(float v) {
+  v += dpp_src<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_src<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_src<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_src<0x140, 0xF>(v);  // row_mirror
+  v += dpp_src<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_src<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QH_WAVE));
