@@ -36,6 +36,10 @@ sys.path.insert(0, ROOT)
 import __graft_entry__  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E peak
+
+
+def log(msg):
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 REFERENCE_TOKS = 53.9            # README.md:50-52 (RTX 5060, real checkpoint)
 
 
@@ -90,6 +94,7 @@ def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
     t0 = time.perf_counter()
     model = orc.OracleModel(w_cpu, max_seq_len=64, prefill="sequential")
     setup = time.perf_counter() - t0
+    log(f"cpu oracle ready ({setup:.0f} s)")
     prompt = synth.make_prompt(w_cpu.cfg, n=n_prompt, seed=7)
     logits = model.forward(prompt, 0).view(-1)
     toks, all_logits = [], [logits]
@@ -100,6 +105,7 @@ def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
         toks.append(t)
         logits, _ = model.decode_token(t, pos)
         logits = logits.view(-1)
+        log(f"cpu step {pos - n_prompt + 1}/{n_steps}")
         all_logits.append(logits)
         pos += 1
     dt = time.perf_counter() - t0
@@ -153,10 +159,12 @@ def main():
 
     cfg = config.qwen35_4b()
     w = synth.make_weights(cfg, seed=args.seed, device="cuda")
+    log("weights built")
     max_seq = 4096
     assert args.prompt + args.warmup + args.steps + 1 <= max_seq
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
     eng.capture()
+    log("decode step captured")
     prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
     eng.prefill(prompt.view(1, -1))
     eng.generate(args.warmup)
@@ -166,11 +174,13 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     toks_per_s = args.steps / dt
+    log(f"timed decode: {toks_per_s:.1f} tok/s")
     ms_per_step = dt * 1e3 / args.steps
     ctx0 = args.prompt + args.warmup
     bytes_tok = w.nbytes_per_token()
 
     mlp_us, n_launch = time_mlp_launches(eng)
+    log(f"gate/up kernel: {mlp_us:.2f} us per launch")
     mbytes = mlp_bytes(cfg)
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
 
@@ -178,7 +188,9 @@ def main():
     cpu = None
     parity = None
     if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) ...")
         tps, threads, setup, p_prompt, o_toks, o_logits = cpu_baseline(w)
+        log(f"cpu baseline: {tps:.4f} tok/s on {threads} threads")
         eng._reset_cache()
         eng.prefill(p_prompt.view(1, -1).cuda())
         eng.generate(len(o_toks) - 1)
