@@ -50,6 +50,19 @@ def mlp_bytes(cfg):
     return w + s + H * 2 + H * 4 + I * 2           # + x, norm weights, output
 
 
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each calibrated on a copy of known size), or None
+    when there is none."""
+    path = os.path.join(ROOT, "profiles", "gate_up_traffic_pmc.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        return int(d["traffic_bytes_per_launch"]), d["kernel"]
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def time_mlp_launches(eng, reps=8):
     """Mean time per launch of the fused gate/up kernel: a captured HIP graph
     of back-to-back launches over every layer's weights (1.5 GB, more than the
@@ -81,6 +94,31 @@ def time_mlp_launches(eng, reps=8):
     torch.cuda.synchronize()
     n = reps * len(eng.w.layers)
     return a.elapsed_time(b) * 1e3 / n, n
+
+
+def traffic_probe(eng, reps=2, copy_mib=256):
+    """Eager launches for counter collection (rocprofv3 --pmc): the gate/up
+    kernel over every layer's weights `reps` times, then a plain device copy
+    of `copy_mib` MiB (known bytes: the calibration of FETCH_SIZE/WRITE_SIZE)."""
+    from qwen35_amd import abi, ops
+    cfg, L = eng.cfg, eng.lib
+    for _ in range(reps):
+        for ly in eng.w.layers:
+            wg, sg = ly["gate_proj"]
+            wu, su = ly["up_proj"]
+            abi.check(L.qh_mlp_gate_up(abi.ptr(eng.h2), None, abi.ptr(ly["post_attention_layernorm"]),
+                                       eng.eps, cfg.hidden_size, abi.ptr(wg), abi.ptr(sg),
+                                       abi.ptr(wu), abi.ptr(su), wg.shape[0],
+                                       ops.scale_mode(wg, sg), abi.ptr(eng.m), None, None, 0,
+                                       abi.stream_handle()), "mlp")
+    src = torch.empty(copy_mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe": True, "mlp_launches": reps * len(eng.w.layers),
+                      "mlp_algorithmic_bytes": mlp_bytes(cfg), "copy_bytes": copy_mib << 20,
+                      "copies": 4}))
 
 
 def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
@@ -145,6 +183,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU (batch-1 decode runs on a single MI355X; "
@@ -163,6 +203,9 @@ def main():
     max_seq = 4096
     assert args.prompt + args.warmup + args.steps + 1 <= max_seq
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
+    if args.traffic_probe:
+        traffic_probe(eng)
+        return
     eng.capture()
     log("decode step captured")
     prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
@@ -182,6 +225,8 @@ def main():
     mlp_us, n_launch = time_mlp_launches(eng)
     log(f"gate/up kernel: {mlp_us:.2f} us per launch")
     mbytes = mlp_bytes(cfg)
+    traffic, tk = measured_traffic()
+    traffic_src = (f"profiles/gate_up_traffic_pmc.json ({tk})" if traffic is not None else None)
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
 
     # short greedy parity sample (GPU engine vs CPU oracle, same weights)
@@ -228,14 +273,15 @@ def main():
             "baseline": "reference README 53.9 tok/s on RTX 5060 (different GPU, real checkpoint)",
         },
         "roofline": {
-            "kernel": "mlp_gate_up_kernel (fused RMSNorm + gate/up E4M3 GEMV + SiLU*up), "
-                      "9216x2560 x2",
+            "kernel": "mlp_fast_kernel<5, 2, float> (fused RMSNorm + gate/up E4M3 GEMV + "
+                      "SiLU*up), 9216x2560 x2",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "algorithmic_bytes_per_launch": mbytes,
             "mean_launch_us": round(mlp_us, 3),
             "launches_timed": n_launch,
