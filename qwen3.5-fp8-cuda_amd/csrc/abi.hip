@@ -606,3 +606,17 @@ QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y,
   if (rc != 0) return -1;
   return check_launch("qh_gemm_e4m3");
 }
+
+// Chained decode phases (no reference counterpart: the reference launches each
+// projection separately, fused_kernels.cu:1156-1195 being its largest fusion).
+// Up to 4 dependent GEMV / gate-up phases in one launch; `sync` holds
+// qh_chain_sync_words() uint32 words, zeroed once before the first launch (the
+// counters only grow; one buffer per call site), `err` (optional) is set to 1
+// if a phase wait expired.
+QH_EXPORT int qh_chain_sync_words(void) { return qh_chain_sync_word_count(); }
+
+QH_EXPORT int qh_chain(const void* phases, int nphase, unsigned* sync, int* err,
+                       hipStream_t stream) {
+  if (qh_launch_chain((const QhChainPhaseDesc*)phases, nphase, sync, err, stream) != 0) return -1;
+  return check_launch("qh_chain");
+}

@@ -16,7 +16,15 @@ Per decode step the GPU runs 5 kernels per layer plus one for the head:
                    position += 1, next token's embedding row.
 Token, position and hidden state stay on the device, so one step is a
 replayable HIP graph with no host round trip.
+
+With use_chain=True (4B shapes only) the launches between two mixers run as
+one chained launch (qh_chain: output projection, gate/up, down, next input
+projection on a persistent grid with device-side phase barriers).  It gives
+bit-identical results but measured slower on MI355X (45.6 vs 33.3 us per
+layer): a grid-wide barrier across the non-coherent per-XCD L2s costs more
+than the kernel boundary it replaces, so separate launches are the default.
 """
+import ctypes
 import math
 
 import torch
@@ -41,7 +49,8 @@ def default_attn_splits(max_seq):
 
 
 class Qwen35FP8Engine:
-    def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda"):
+    def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda",
+                 use_chain=False):
         if not torch.cuda.is_available():
             raise RuntimeError("Qwen35FP8Engine needs a GPU (there is no CPU fallback)")
         self.lib = abi.load()
@@ -97,6 +106,15 @@ class Qwen35FP8Engine:
                                               device=dev))
         self.graph = None
         self.prompt_buf = None
+        # Chained launches (qh_chain): per layer, the mixer's output projection,
+        # gate/up, down and the next layer's input projection run as one launch.
+        self.use_chain = use_chain and self._chain_shapes_ok()
+        if self.use_chain:
+            words = int(self.lib.qh_chain_sync_words())
+            self.chain_sync = torch.zeros(cfg.num_hidden_layers, words, dtype=torch.int32,
+                                          device=dev)
+            self.chain_err = torch.zeros(1, dtype=torch.int32, device=dev)
+            self.chains = [self._build_chain(i) for i in range(cfg.num_hidden_layers)]
 
     # ------------------------------------------------------------------ state
     def _reset_cache(self):
@@ -124,12 +142,64 @@ class Qwen35FP8Engine:
                                  abi.ptr(res), None, len(segs), *args, 0, abi.stream_handle()),
                   "gemv")
 
-    def _layer(self, i):
+    def _in_segs(self, i):
+        """Input projection of layer i: ((w, s), out) segments sharing the
+        normalised hidden state."""
+        ly = self.w.layers[i]
+        if self.cfg.is_full(i):
+            return [(ly["q_proj"], self.q_all), (ly["k_proj"], self.k_new),
+                    (ly["v_proj"], self.v_new)]
+        return [(ly["in_proj_qkv"], self.mixed), (ly["in_proj_z"], self.z),
+                (ly["in_proj_a"], self.a), (ly["in_proj_b"], self.b)]
+
+    def _out_proj(self, i):
+        ly = self.w.layers[i]
+        if self.cfg.is_full(i):
+            return self.mix_out[:self.cfg.attn_out_dim], ly["o_proj"]
+        return self.mix_out[:self.cfg.value_dim], ly["out_proj"]
+
+    def _chain_shapes_ok(self):
+        """qh_chain's fast-path shapes: hidden 2560, output-projection K 4096,
+        MLP 9216, fp32 128x128 block scales everywhere."""
+        cfg = self.cfg
+        if (cfg.hidden_size, cfg.intermediate_size) != (2560, 9216):
+            return False
+        for i in range(cfg.num_hidden_layers):
+            x, wo = self._out_proj(i)
+            mats = [wo, self.w.layers[i]["gate_proj"], self.w.layers[i]["up_proj"],
+                    self.w.layers[i]["down_proj"]] + [ws for ws, _ in self._in_segs(i)]
+            if x.numel() != 4096:
+                return False
+            for w, s in mats:
+                if s.dtype != torch.float32 or s.dim() != 2 or s.shape[1] * 128 != w.shape[1] \
+                        or s.shape[0] != (w.shape[0] + 127) // 128:
+                    return False
+        return True
+
+    def _build_chain(self, i):
+        """Phases of layer i's chain: output projection (+ residual h -> h2),
+        gate/up (h2 -> m), down (+ residual h2 -> h), then layer i+1's input
+        projection (h -> q/k/v or qkv/z/a/b) unless i is the last layer."""
+        ly = self.w.layers[i]
+        x, wo = self._out_proj(i)
+        ph = [ops.chain_gemv_phase(x, [(wo, self.h2)], res=self.h, eps=self.eps),
+              ops.chain_mlp_phase(self.h2, ly["post_attention_layernorm"], ly["gate_proj"],
+                                  ly["up_proj"], self.m, eps=self.eps),
+              ops.chain_gemv_phase(self.m, [(ly["down_proj"], self.h)], res=self.h2, eps=self.eps)]
+        if i + 1 < self.cfg.num_hidden_layers:
+            ph.append(ops.chain_gemv_phase(self.h, self._in_segs(i + 1),
+                                           norm_w=self.w.layers[i + 1]["input_layernorm"],
+                                           eps=self.eps))
+        return (abi.ChainPhase * len(ph))(*ph)
+
+    def chain_error(self):
+        """True if a chained launch's bounded wait expired (results invalid)."""
+        return self.use_chain and int(self.chain_err.item()) != 0
+
+    def _mixer(self, i):
         cfg, L, ly = self.cfg, self.lib, self.w.layers[i]
         st = abi.stream_handle()
         if cfg.is_full(i):
-            self._gemv(self.h, [(ly["q_proj"], self.q_all), (ly["k_proj"], self.k_new),
-                                (ly["v_proj"], self.v_new)], norm_w=ly["input_layernorm"])
             D = cfg.head_dim
             gate = self.q_all[D:]
             abi.check(L.qh_attn_decode(
@@ -140,11 +210,7 @@ class Qwen35FP8Engine:
                 cfg.num_attention_heads, cfg.num_key_value_heads, abi.ptr(self.pos), 0,
                 self.attn_splits, abi.ptr(self.attn_scratch), abi.ptr(self.attn_counters),
                 abi.ptr(self.mix_out), self.eps, st), "attn_decode")
-            self._gemv(self.mix_out[:cfg.attn_out_dim], [(ly["o_proj"], self.h2)], res=self.h)
         else:
-            self._gemv(self.h, [(ly["in_proj_qkv"], self.mixed), (ly["in_proj_z"], self.z),
-                                (ly["in_proj_a"], self.a), (ly["in_proj_b"], self.b)],
-                       norm_w=ly["input_layernorm"])
             abi.check(L.qh_gdn_decode(
                 abi.ptr(self.mixed), abi.ptr(self.a), abi.ptr(self.b), abi.ptr(self.z),
                 abi.ptr(self.conv_ring[i]), abi.ptr(ly["conv1d_w"]), abi.ptr(ly["A_log"]),
@@ -152,7 +218,13 @@ class Qwen35FP8Engine:
                 abi.ptr(self.core), abi.ptr(self.mix_out), abi.ptr(self.gdn_counters),
                 abi.ptr(self.pos), 0, cfg.linear_num_key_heads, cfg.linear_num_value_heads,
                 cfg.linear_key_head_dim, cfg.linear_value_head_dim, self.eps, st), "gdn_decode")
-            self._gemv(self.mix_out[:cfg.value_dim], [(ly["out_proj"], self.h2)], res=self.h)
+
+    def _post(self, i):
+        """Output projection + residual, gate/up, down + residual (separate launches)."""
+        cfg, L, ly = self.cfg, self.lib, self.w.layers[i]
+        st = abi.stream_handle()
+        x, wo = self._out_proj(i)
+        self._gemv(x, [(wo, self.h2)], res=self.h)
         wg, sg = ly["gate_proj"]
         wu, su = ly["up_proj"]
         abi.check(L.qh_mlp_gate_up(abi.ptr(self.h2), None, abi.ptr(ly["post_attention_layernorm"]),
@@ -171,12 +243,26 @@ class Qwen35FP8Engine:
             abi.ptr(self.w.embed) if next_embed else None,
             abi.ptr(self.h) if next_embed else None, abi.stream_handle()), "lm_head_argmax")
 
+    def _pre(self, i):
+        self._gemv(self.h, self._in_segs(i), norm_w=self.w.layers[i]["input_layernorm"])
+
     def decode_step_launches(self):
         """Enqueue one decode step on the current stream: h holds the input
         token's embedding, pos its position; afterwards logits/tok hold the
         result, h the next token's embedding and pos = pos + 1."""
-        for i in range(self.cfg.num_hidden_layers):
-            self._layer(i)
+        n = self.cfg.num_hidden_layers
+        self._pre(0)
+        for i in range(n):
+            self._mixer(i)
+            if self.use_chain:
+                arr = self.chains[i]
+                abi.check(self.lib.qh_chain(ctypes.cast(arr, ctypes.c_void_p), len(arr),
+                                            abi.ptr(self.chain_sync[i]), abi.ptr(self.chain_err),
+                                            abi.stream_handle()), "qh_chain")
+            else:
+                self._post(i)
+                if i + 1 < n:
+                    self._pre(i + 1)
         self._head()
 
     # ------------------------------------------------------------ graphs
