@@ -47,6 +47,40 @@ __device__ __forceinline__ void store_head(uint16_t* dst, const float (&v)[NPL])
   }
 }
 
+// A head's D fp32 values (lane l holds NPL consecutive ones at l * NPL),
+// written / read with one device-coherent (sc1) buffer access per lane: split
+// partials pass between workgroups that may sit on different XCDs, whose L2
+// caches are not coherent.  `head` is wave-uniform (the buffer resource lives
+// in scalar registers); the lane offset goes in the vector offset.
+template <int NPL>
+__device__ __forceinline__ void store_head_f32_coherent(float* head, int lane, const float (&v)[NPL]) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(head, (short)0, (int)(64 * NPL * 4), 0x00020000);
+  const uint32_t off = (uint32_t)lane * NPL * 4u;
+  if constexpr (NPL == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])},
+        r, off, 0, 16);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(v[0]), __float_as_uint(v[1])}, r, off, 0,
+                                          16);
+  }
+}
+template <int NPL>
+__device__ __forceinline__ void load_head_f32_coherent(float (&v)[NPL], const float* head, int lane) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(head), (short)0, (int)(64 * NPL * 4), 0x00020000);
+  const uint32_t off = (uint32_t)lane * NPL * 4u;
+  if constexpr (NPL == 4) {
+    const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y);
+    v[2] = __uint_as_float(u.z); v[3] = __uint_as_float(u.w);
+  } else {
+    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16);
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y);
+  }
+}
+
 // bf16 (1+w) RMSNorm over a D-wide head held NPL values per lane, then bf16
 // partial RoPE.  All lanes of the wave must call this.
 template <int D>
@@ -111,6 +145,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   span = ((span + TP - 1) / TP) * TP;
   const int p0 = split * span;
   const int p1 = min(total, p0 + span);
+  // Splits past the context do nothing and do not take part in the merge:
+  // the arrival target is the number of splits that hold positions (the same
+  // value in every workgroup, computed from the device position).
+  const int nactive = (total + span - 1) / span;
+  const bool slot_in_range0 = slot >= 0 && slot < total;
+  if (p.nsplit > 1 && split >= nactive && !(split == 0 && !slot_in_range0)) return;
   const bool slot_in_range = slot >= 0 && slot < total;
   const bool owner = (slot >= p0 && slot < p1) || (split == 0 && !slot_in_range);
   const float* cos_row = p.cos_t + (size_t)rope_pos * p.rot;
@@ -155,6 +195,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     }
   };
   if (p0 < p1) fetch(p0);
+
+  // Output gate values of this wave's heads, loaded now (they are needed only
+  // by the workgroup that emits, after the merge).
+  float gate_v[HPW][NPL];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi;
+    if (p.gate && gi < G)
+      load_head<NPL>(gate_v[hi], p.gate + (size_t)(kvh * G + gi) * p.gate_stride + lane * NPL);
+  }
 
   // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
   for (int gi = wid; gi < G; gi += 4) {
@@ -245,16 +295,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     __syncthreads();
   }
 
-  auto emit = [&](int gi, float (&ov)[NPL], float inv) {
+  auto emit = [&](int gi, const float (&gv)[NPL], float (&ov)[NPL], float inv) {
     const int h = kvh * G + gi;
     float r[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       float a = ov[i] * inv;
-      if (p.gate) {
-        const float gv = bf2f(p.gate[(size_t)h * p.gate_stride + lane * NPL + i]);
-        a = rbf(a) * rbf(qh_sigmoid(gv));
-      }
+      if (p.gate) a = rbf(a) * rbf(qh_sigmoid(gv[i]));
       r[i] = a;
     }
     store_head<NPL>(p.out + (size_t)h * D + lane * NPL, r);
@@ -264,7 +311,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
       const int gi = wid + 4 * hi;
-      if (gi < G) emit(gi, o[hi], 1.0f / l[hi]);
+      if (gi < G) emit(gi, gate_v[hi], o[hi], 1.0f / l[hi]);
     }
     return;
   }
@@ -276,15 +323,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     const int gi = wid + 4 * hi;
     if (gi < G) {
       float* dst = p.part + ((size_t)(kvh * p.nsplit + split) * MAXG + gi) * rec;
-#pragma unroll
-      for (int i = 0; i < NPL; ++i) pub_store(dst + lane * NPL + i, o[hi][i]);
+      store_head_f32_coherent<NPL>(dst, lane, o[hi]);
       if (lane == 0) {
         pub_store(dst + D, m[hi]);
         pub_store(dst + D + 1, l[hi]);
       }
     }
   }
-  if (!arrive_last(p.counters + kvh, (unsigned)p.nsplit, &s_last)) return;
+  if (!arrive_last(p.counters + kvh, (unsigned)nactive, &s_last)) return;
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
     const int gi = wid + 4 * hi;
@@ -292,7 +338,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     const float* base = p.part + ((size_t)kvh * p.nsplit * MAXG + gi) * rec;
     const size_t sstride = (size_t)MAXG * rec;
     // lane s holds split s's (m, l); nsplit <= 64 (checked on the host)
-    const bool have = lane < p.nsplit;
+    const bool have = lane < nactive;
     const float ls = have ? pub_load(base + lane * sstride + D + 1) : 0.0f;
     const float ms = have ? pub_load(base + lane * sstride + D) : -INFINITY;
     const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
@@ -301,14 +347,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     float acc[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
-    for (int s = 0; s < p.nsplit; ++s) {
+    for (int s = 0; s < nactive; ++s) {
       const float w = __shfl(ws, s, 64);
       if (w == 0.0f) continue;  // uniform: empty split
-      const float* src = base + s * sstride + lane * NPL;
+      float part[NPL];
+      load_head_f32_coherent<NPL>(part, base + s * sstride, lane);
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) acc[i] = fmaf(pub_load(src + i), w, acc[i]);
+      for (int i = 0; i < NPL; ++i) acc[i] = fmaf(part[i], w, acc[i]);
     }
-    emit(gi, acc, 1.0f / L);
+    emit(gi, gate_v[hi], acc, 1.0f / L);
   }
   if (threadIdx.x == 0) reset_counter(p.counters + kvh);
 }

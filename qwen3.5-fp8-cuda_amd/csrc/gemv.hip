@@ -529,10 +529,17 @@ __attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void mlp_gate_up_kerne
 // is a few scalar instructions; the scales of the row's 128-row block come
 // the same way (lane l, chunk j reads k-block 4j + l/16).  Row totals are
 // reduced with DPP moves into a wave-uniform value.
+// Scale registers per row: lane l holds the fp32 scale of k-block l (and
+// 64 + l when K > 8192) of the row's 128-row block; a chunk's scale (k-block
+// 4j + l/16) is fetched with ds_bpermute, which runs on the LDS crossbar and
+// so takes no slot of the vector-memory counter the weight pipeline lives on.
+template <int CPL>
+constexpr int scale_regs() { return (CPL * 4 + 63) / 64; }
+
 template <int CPL, typename ScaleT>
-__device__ __forceinline__ void issue_fast(u32x2 (&w)[CPL], float (&sc)[CPL], const uint8_t* W,
-                                           const void* S, int row, bool valid, uint32_t lw,
-                                           uint32_t ls) {
+__device__ __forceinline__ void issue_fast(u32x2 (&w)[CPL], float (&sr_)[scale_regs<CPL>()],
+                                           const uint8_t* W, const void* S, int row, bool valid,
+                                           uint32_t lw, uint32_t lane) {
   constexpr int K = CPL * 512, KB = K / 128;
   const qh_rsrc wr = make_rsrc(W + (size_t)row * K, valid ? (uint32_t)K : 0u);
   const qh_rsrc sr = make_rsrc((const ScaleT*)S + (size_t)(row >> 7) * KB,
@@ -540,21 +547,27 @@ __device__ __forceinline__ void issue_fast(u32x2 (&w)[CPL], float (&sc)[CPL], co
 #pragma unroll
   for (int j = 0; j < CPL; ++j) w[j] = bload_w8(wr, lw + 512u * j);
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const uint32_t off = ls + (uint32_t)(4 * j * sizeof(ScaleT));
+  for (int r = 0; r < scale_regs<CPL>(); ++r) {
+    const uint32_t off = (lane + 64u * r) * (uint32_t)sizeof(ScaleT);
     if (sizeof(ScaleT) == 4)
-      sc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
+      sr_[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
     else
-      sc[j] = bf2f(bload_u16(sr, off));
+      sr_[r] = bf2f(bload_u16(sr, off));
   }
 }
 
 template <int CPL, bool XLDS>
-__device__ __forceinline__ float dot_row(const u32x2 (&w)[CPL], const float (&sc)[CPL],
-                                         const XSlice<CPL, XLDS>& xs) {
+__device__ __forceinline__ float dot_row(const u32x2 (&w)[CPL], const float (&sr_)[scale_regs<CPL>()],
+                                         const XSlice<CPL, XLDS>& xs, uint32_t q4) {
   float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) acc = fmaf(dot8_e4m3_bf16(w[j].x, w[j].y, xs[j], 0.0f), sc[j], acc);
+  for (int j = 0; j < CPL; ++j) {
+    // k-block 4j + lane/16 lives in lane (4j + lane/16) % 64 of register j/16
+    const float sc = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((int)(((4u * j) & 63u) * 4u + q4),
+                                            __builtin_bit_cast(int, sr_[j >> 4])));
+    acc = fmaf(dot8_e4m3_bf16(w[j].x, w[j].y, xs[j], 0.0f), sc, acc);
+  }
   return acc;
 }
 
@@ -619,22 +632,22 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
   constexpr int K = CPL * 512;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t lw = lane * 8u, ls = (uint32_t)((lane >> 4) * sizeof(ScaleT));
+  const uint32_t lw = lane * 8u, q4 = (uint32_t)(lane >> 4) * 4u;
   const int stride = nwg * 4;
   int g = wg * 4 + wid;
 
   u32x2 w[P][CPL];
-  float sc[P][CPL];
+  float sc[P][scale_regs<CPL>()];
   float res[P];
   int srow[P], sseg[P];
-  auto issue_w = [&](u32x2 (&w_)[CPL], float (&sc_)[CPL], int& row_, int& seg_, int gg) {
+  auto issue_w = [&](u32x2 (&w_)[CPL], float (&sc_)[scale_regs<CPL>()], int& row_, int& seg_, int gg) {
     int si = 0;
 #pragma unroll
     for (int t = 1; t < 4; ++t)
       if (t < p.nseg && gg >= p.gstart[t]) si = t;
     row_ = gg - p.gstart[si];
     seg_ = si;
-    issue_fast<CPL, ScaleT>(w_, sc_, p.seg[si].w, p.seg[si].s, row_, gg < p.gtotal, lw, ls);
+    issue_fast<CPL, ScaleT>(w_, sc_, p.seg[si].w, p.seg[si].s, row_, gg < p.gtotal, lw, lane);
   };
   auto issue_res = [&](float& res_, int row_, int gg) {
     if (p.res1) {
@@ -673,7 +686,7 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       if (g >= p.gtotal) return;
-      const float acc = wave_total(dot_row<CPL>(w[s], sc[s], xs));
+      const float acc = wave_total(dot_row<CPL>(w[s], sc[s], xs, q4));
       if (lane == 0) {
         float y = rbf(acc);
         if (p.res1) y = res[s] + y;
@@ -694,19 +707,19 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
   constexpr int K = CPL * 512;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t lw = lane * 8u, ls = (uint32_t)((lane >> 4) * sizeof(ScaleT));
+  const uint32_t lw = lane * 8u, q4 = (uint32_t)(lane >> 4) * 4u;
   const int stride = nwg * 4;
   int g = wg * 4 + wid;
 
   XIn<CPL> xin;
   if (!CH && early_x<CPL>()) block_x_load<CPL, CH>(xin, p.x, p.x2, p.norm_w, K);
   u32x2 wg_[P][CPL], wu[P][CPL];
-  float sg[P][CPL], su[P][CPL];
+  float sg[P][scale_regs<CPL>()], su[P][scale_regs<CPL>()];
 #pragma unroll
   for (int s = 0; s < P; ++s) {
     const int gg = g + s * stride;
-    issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gg, gg < p.N, lw, ls);
-    issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gg, gg < p.N, lw, ls);
+    issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gg, gg < p.N, lw, lane);
+    issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gg, gg < p.N, lw, lane);
   }
   if (CH) {
     chain_wait(wt);
@@ -723,8 +736,8 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       if (g >= p.N) return;
-      const float ag = wave_total(dot_row<CPL>(wg_[s], sg[s], xs));
-      const float au = wave_total(dot_row<CPL>(wu[s], su[s], xs));
+      const float ag = wave_total(dot_row<CPL>(wg_[s], sg[s], xs, q4));
+      const float au = wave_total(dot_row<CPL>(wu[s], su[s], xs, q4));
       if (lane == 0) {
         // SiLU on the fp32 accumulators (fused_kernels.cu:476).
         st_act1<OUTC>(p.m_out + g, f2bf(qh_silu(ag) * au));
@@ -732,8 +745,8 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
         if (p.u_out) st_act1<OUTC>(p.u_out + g, f2bf(au));
       }
       const int gn = g + P * stride;
-      issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gn, gn < p.N, lw, ls);
-      issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gn, gn < p.N, lw, ls);
+      issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gn, gn < p.N, lw, lane);
+      issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gn, gn < p.N, lw, lane);
       g += stride;
     }
   }
@@ -816,7 +829,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
       // inputs (written by earlier launches), coherent outputs.
       const QhWait none = {nullptr, 0ull, nullptr};
       switch (c.kind[0] * 64 + c.cpl[0]) {
-        case kPhGemv * 64 + 5: gemv_fast_body<5, 2, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
+        case kPhGemv * 64 + 5: gemv_fast_body<5, 4, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
         case kPhGemv * 64 + 8: gemv_fast_body<8, 1, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
         case kPhGemv * 64 + 18: gemv_fast_body<18, 1, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
         case kPhMlp * 64 + 5: mlp_fast_body<5, 2, float, false, true>(c.m[0], wg, nwg, sx, red, none); break;
@@ -825,7 +838,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     } else {
       const QhWait wt = {chain_phase_parts(c.sync, k - 1), (s_epoch + 1ull) * (unsigned)nwg, c.err};
       switch (c.kind[k] * 64 + c.cpl[k]) {
-        case kPhGemv * 64 + 5: gemv_fast_body<5, 2, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
+        case kPhGemv * 64 + 5: gemv_fast_body<5, 4, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
         case kPhGemv * 64 + 8: gemv_fast_body<8, 1, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
         case kPhGemv * 64 + 18: gemv_fast_body<18, 1, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
         case kPhMlp * 64 + 5: mlp_fast_body<5, 2, float, true>(c.m[k], wg, nwg, sx, red, wt); break;
@@ -973,7 +986,8 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
 // slice lives in registers (K <= 4096), one above.
 constexpr int gemv_rows(int cpl) { return cpl > 0 ? 1 : 1; }
 constexpr int gemv_depth(int cpl) { return cpl > 0 ? 1 : 1; }
-constexpr int fast_depth(int cpl) { return cpl <= 6 ? 2 : 1; }
+constexpr int fast_depth(int cpl) { return cpl <= 6 ? 4 : 1; }
+constexpr int mlp_fast_depth(int cpl) { return cpl <= 6 ? 2 : 1; }
 constexpr uint32_t kMaxBufferBytes = 0x7fffffffu;
 
 int cu_count() {
@@ -1035,7 +1049,7 @@ void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
 
 template <int CPL, typename ScaleT>
 void launch_mlp_fast_t(const QhMlpParams& p, hipStream_t st) {
-  auto fn = mlp_fast_kernel<CPL, fast_depth(CPL), ScaleT>;
+  auto fn = mlp_fast_kernel<CPL, mlp_fast_depth(CPL), ScaleT>;
   const int grid = std::max(1, std::min({resident_blocks((const void*)fn), 2 * cu_count(), (p.N + 3) / 4}));
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
