@@ -82,47 +82,54 @@ __device__ __forceinline__ float half_block_sum(float v, float* red2) {
   return red2[base] + red2[base + 1];
 }
 
+// One 512-thread workgroup per value head (dk = dv = 128): thread t owns value
+// column j = t & 127 and state rows 32 (t >> 7) .. +32 of it, so the head's
+// 64 KB of state is requested at once, first thing, and the gated RMSNorm
+// over the head's 128 outputs is a block reduction (no cross-workgroup
+// hand-off).  The q/k conv + l2norm of the key head is recomputed per value
+// head (256 channels, cheap).
+constexpr int GDN_THREADS = 512;
+
 template <int DK>
-__global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
-  static_assert(DK == 128, "fused decode step assumes dk = 128");
-  __shared__ float qn[DK], kn[DK];
-  __shared__ float red[8 * 32];
-  __shared__ float red2[4];
-  __shared__ float vconv[VS];
-  __shared__ int s_last;
+__global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) {
+  static_assert(DK == 128, "fused decode step assumes dk = dv = 128");
+  constexpr int DV = 128, RG = GDN_THREADS / DV, RPT = DK / RG;  // 4 row groups x 32 rows
+  __shared__ float qn[DK], kn[DK], vconv[DV];
+  __shared__ float red[RG][DV];
+  __shared__ float red2[8];
 
   const int h = blockIdx.x;
-  const int sidx = blockIdx.y;
   const int r = p.Hv / p.Hk;
   const int kh = h / r;
   const int t = p.pos_dev ? *p.pos_dev : p.pos;
-  const int dv = p.dv;
   const int tid = threadIdx.x;
-  // The state columns are the bulk of the traffic: request them first.
-  float* cols = p.state + (size_t)h * DK * dv + sidx * VS;
-  float S[DK / 8];
-  load_columns<DK>(S, cols, dv);
+  const int j = tid & (DV - 1);
+  const int rg = tid >> 7;
+  const int lane = tid & 63, wid = tid >> 6;
 
-  // ---- causal conv (window of 4) + SiLU for q/k of key head kh ------------
-  {
-    const int i = tid & (DK - 1);
-    const bool is_k = tid >= DK;
-    const int c = (is_k ? p.Hk * DK : 0) + kh * DK + i;
-    const uint16_t x_t = p.mixed[c];
-    const uint16_t* ring = p.conv_ring + (size_t)c * 4;
-    const uint16_t* w = p.conv_w + (size_t)c * 4;
-    float acc = bf2f(w[3]) * bf2f(x_t);
-    acc = fmaf(bf2f(w[2]), bf2f(ring[(t + 3) & 3]), acc);
-    acc = fmaf(bf2f(w[1]), bf2f(ring[(t + 2) & 3]), acc);
-    acc = fmaf(bf2f(w[0]), bf2f(ring[(t + 1) & 3]), acc);
-    const float y = rbf(qh_silu(rbf(acc)));
-    if (sidx == 0 && (h % r) == 0) p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
-    const float ss = half_block_sum(y * y, red2);
-    if (is_k) kn[i] = y * rsqrtf(ss + 1e-6f);
-    else qn[i] = y * rsqrtf(ss + 1e-6f) * rsqrtf((float)DK);
+  // The state is the bulk of the traffic: request it first.
+  float* cols = p.state + (size_t)h * DK * DV + j;
+  float S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) S[i] = cols[(size_t)(rg * RPT + i) * DV];
+  // Operands of the output norm, needed last, requested early.
+  float zv = 0.0f, nw = 0.0f;
+  if (rg == 0) {
+    zv = bf2f(p.z[(size_t)h * DV + j]);
+    nw = bf2f(p.norm_w[j]);
   }
-  if (tid < VS) {
-    const int c = 2 * p.Hk * DK + h * dv + sidx * VS + tid;
+
+  // ---- causal conv (window of 4) + SiLU: q/k of key head kh (threads
+  // 0..255), v of value head h (256..383) ------------------------------------
+  float y = 0.0f;
+  int c = -1;
+  if (tid < 2 * DK) {
+    const bool is_k = tid >= DK;
+    c = (is_k ? p.Hk * DK : 0) + kh * DK + (tid & (DK - 1));
+  } else if (tid < 2 * DK + DV) {
+    c = 2 * p.Hk * DK + h * DV + (tid - 2 * DK);
+  }
+  if (c >= 0) {
     const uint16_t x_t = p.mixed[c];
     const uint16_t* ring = p.conv_ring + (size_t)c * 4;
     const uint16_t* w = p.conv_w + (size_t)c * 4;
@@ -130,8 +137,21 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
     acc = fmaf(bf2f(w[2]), bf2f(ring[(t + 3) & 3]), acc);
     acc = fmaf(bf2f(w[1]), bf2f(ring[(t + 2) & 3]), acc);
     acc = fmaf(bf2f(w[0]), bf2f(ring[(t + 1) & 3]), acc);
-    vconv[tid] = rbf(qh_silu(rbf(acc)));
-    p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
+    y = rbf(qh_silu(rbf(acc)));
+    // q/k channels are shared by the r value heads of a key head: one writes.
+    if (tid >= 2 * DK || (h % r) == 0) p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
+  }
+  // l2norm of q (waves 0-1) and k (waves 2-3)
+  float ss = wave_sum(y * y);
+  if (lane == 0) red2[wid] = ss;
+  __syncthreads();
+  if (tid < 2 * DK) {
+    const int base = (wid >> 1) * 2;
+    const float n = red2[base] + red2[base + 1];
+    if (tid >= DK) kn[tid - DK] = y * rsqrtf(n + 1e-6f);
+    else qn[tid] = y * rsqrtf(n + 1e-6f) * rsqrtf((float)DK);
+  } else if (tid < 2 * DK + DV) {
+    vconv[tid - 2 * DK] = y;
   }
   // ---- gates ----------------------------------------------------------------
   const float beta = rbf(qh_sigmoid(bf2f(p.b[h])));
@@ -139,34 +159,39 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(QhGdnParams p) {
   const float decay = __expf(g);
   __syncthreads();
 
-  const float o = delta_columns<DK>(S, cols, dv, qn, kn, vconv[tid & 31], beta, decay, red);
-  const int j = tid & 31;
-  // core = bf16(o), published as fp32 for the head's last column workgroup
-  if (tid < 32) pub_store(p.core + (size_t)h * dv + sidx * VS + j, rbf(o));
-
-  // ---- gated RMSNorm by the last column workgroup of this head ------------
-  const int nslice = dv / VS;
-  if (nslice > 1) {
-    if (!arrive_last(p.counters + h, (unsigned)nslice, &s_last)) return;
-  } else {
-    wait_mem();
-    __syncthreads();
-  }
-  // dv <= 256: one element per thread
-  const bool ok = tid < dv;
-  const float x = ok ? pub_load(p.core + (size_t)h * dv + tid) : 0.0f;
-  float ss = wave_sum(x * x);
+  // ---- delta rule on column j ---------------------------------------------
+  float pred = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) pred = fmaf(S[i] * decay, kn[rg * RPT + i], pred);
+  red[rg][j] = pred;
   __syncthreads();
-  if ((tid & 63) == 0) red2[tid >> 6] = ss;
-  __syncthreads();
-  ss = red2[0] + red2[1] + red2[2] + red2[3];
-  if (ok) {
-    const float rs = rsqrtf(ss / (float)dv + p.eps);
-    const float normed = rbf(rbf(x * rs) * bf2f(p.norm_w[tid]));
-    const float sz = rbf(qh_silu(bf2f(p.z[(size_t)h * dv + tid])));
-    p.out[(size_t)h * dv + tid] = f2bf(normed * sz);
+  pred = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+  const float delta = (vconv[j] - pred) * beta;
+  float o = 0.0f;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const float upd = fmaf(kn[rg * RPT + i], delta, S[i] * decay);
+    cols[(size_t)(rg * RPT + i) * DV] = upd;
+    o = fmaf(upd, qn[rg * RPT + i], o);
   }
-  if (nslice > 1 && tid == 0) reset_counter(p.counters + h);
+  __syncthreads();
+  red[rg][j] = o;
+  __syncthreads();
+  // ---- gated RMSNorm over the head (threads 0..127 = waves 0, 1) ------------
+  float core = 0.0f;
+  if (rg == 0) {
+    core = rbf(red[0][j] + red[1][j] + red[2][j] + red[3][j]);
+    if (p.core) p.core[(size_t)h * DV + j] = core;  // optional: the bf16-rounded core
+    const float sq = wave_sum(core * core);
+    if (lane == 0) red2[wid] = sq;
+  }
+  __syncthreads();
+  if (rg == 0) {
+    const float rs = rsqrtf((red2[0] + red2[1]) / (float)DV + p.eps);
+    const float normed = rbf(rbf(core * rs) * nw);
+    const float sz = rbf(qh_silu(zv));
+    p.out[(size_t)h * DV + j] = f2bf(normed * sz);
+  }
 }
 
 // Reference ABI delta rule (fused_kernels.cu:623-684): q, k already expanded to
@@ -216,16 +241,12 @@ __global__ __launch_bounds__(256) void delta_rule_kernel(const uint16_t* q, cons
 }  // namespace
 
 int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st) {
-  if (p.dk != 128 || p.dv % VS != 0 || p.dv > 256 || p.Hk <= 0 || p.Hv % p.Hk != 0) {
-    qh_set_error("gdn: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk=128, dv%%32==0, dv<=256)",
-                 p.dk, p.dv, p.Hk, p.Hv);
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0) {
+    qh_set_error("gdn: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk = dv = 128)", p.dk, p.dv,
+                 p.Hk, p.Hv);
     return -1;
   }
-  if (p.dv / VS > 1 && !p.counters) {
-    qh_set_error("gdn: counters required");
-    return -1;
-  }
-  hipLaunchKernelGGL(gdn_decode_kernel<128>, dim3(p.Hv, p.dv / VS), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(gdn_decode_kernel<128>, dim3(p.Hv), dim3(GDN_THREADS), 0, st, p);
   return 0;
 }
 

@@ -15,9 +15,9 @@ struct QhGdnParams {
   const float* dt_bias;     // [Hv]
   const uint16_t* norm_w;   // [dv] bf16 (plain weight)
   float* state;             // [Hv, dk, dv] fp32, updated in place
-  float* core;              // [Hv * dv] fp32 scratch: bf16-rounded delta-rule output
+  float* core;              // optional [Hv * dv] fp32: the bf16-rounded delta-rule output
   uint16_t* out;            // [Hv * dv] bf16 gated output
-  unsigned* counters;       // [Hv] zero-initialised arrival counters
+  unsigned* counters;       // unused (kept for the entry point's signature)
   const int* pos_dev;       // optional device position t
   int pos;                  // host position when pos_dev is null
   int Hk, Hv, dk, dv;
