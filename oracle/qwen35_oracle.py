@@ -135,11 +135,13 @@ def mlp_prefill(xn, Wg, Wu, Wd):
 
 # ------------------------------------------------------------ A4 attention
 def rope_tables(max_pos, rot, theta):
-    """fp32 cos/sin [max_pos, rot]; inv_freq over the rotary dim (main.py:527-533)."""
-    inv = 1.0 / (theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot))
-    f = torch.outer(torch.arange(max_pos, dtype=torch.float64), inv)
+    """fp32 cos/sin [max_pos, rot], built in fp32 exactly as main.py:527-533:
+    inv_freq = 1 / theta^(arange(0, rot, 2) / rot), freqs = outer(pos, inv_freq),
+    emb = cat(freqs, freqs)."""
+    inv = 1.0 / (theta ** (torch.arange(0, rot, 2).float() / rot))
+    f = torch.outer(torch.arange(max_pos).float(), inv)
     emb = torch.cat([f, f], dim=-1)
-    return emb.cos().float(), emb.sin().float()
+    return emb.cos().contiguous(), emb.sin().contiguous()
 
 
 def rope_rows(x, cos_row, sin_row, rot, round_out):

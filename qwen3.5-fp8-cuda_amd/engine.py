@@ -33,15 +33,15 @@ from . import abi
 from . import ops
 
 
-def rope_tables(max_pos, rotary_dim, theta):
-    """fp32 cos/sin [max_pos, rotary_dim] of the partial rotary embedding
-    (main.py:513-533: inv_freq denominator is the rotary dim, emb = cat(f, f)),
-    computed in float64 and rounded once."""
-    inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float64) / rotary_dim))
-    pos = torch.arange(max_pos, dtype=torch.float64)
+def rope_tables(max_pos, rotary_dim, theta, device="cpu"):
+    """fp32 cos/sin [max_pos, rotary_dim] of the partial rotary embedding, built
+    in fp32 on `device` the way main.py:527-533 builds it (inv_freq over the
+    rotary dim, freqs = outer(pos, inv_freq), emb = cat(f, f))."""
+    inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, device=device).float() / rotary_dim))
+    pos = torch.arange(max_pos, device=device).float()
     f = torch.outer(pos, inv)
     emb = torch.cat([f, f], dim=-1)
-    return emb.cos().float().contiguous(), emb.sin().float().contiguous()
+    return emb.cos().contiguous(), emb.sin().contiguous()
 
 
 def default_attn_splits(max_seq):
@@ -87,8 +87,8 @@ class Qwen35FP8Engine:
         self.attn_scratch = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=dev)
         self.attn_counters = torch.zeros(cfg.num_key_value_heads, dtype=torch.int32, device=dev)
         self.gdn_counters = torch.zeros(cfg.linear_num_value_heads, dtype=torch.int32, device=dev)
-        cos, sin = rope_tables(max_seq_len, cfg.rotary_dim, cfg.rope_theta)
-        self.rope_cos, self.rope_sin = cos.to(dev), sin.to(dev)
+        self.rope_cos, self.rope_sin = rope_tables(max_seq_len, cfg.rotary_dim, cfg.rope_theta,
+                                                   device=dev)
         self.k_cache, self.v_cache, self.conv_ring, self.state = [], [], [], []
         for i in range(cfg.num_hidden_layers):
             if cfg.is_full(i):
