@@ -113,6 +113,20 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Block-wide sum for an NT-thread block; `red` must hold >= NT/64 floats of LDS.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) s += red[w];
+  return s;
+}
+
 // Block-wide sum for a 256-thread block; `red` must hold >= 4 floats of LDS.
 __device__ __forceinline__ float block_sum_256(float v, float* red) {
   v = wave_sum(v);
