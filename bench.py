@@ -130,7 +130,7 @@ def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
     torch.set_num_threads(os.cpu_count() or 1)
     w_cpu = w_gpu.to("cpu")
     t0 = time.perf_counter()
-    model = orc.OracleModel(w_cpu, max_seq_len=64, prefill="sequential")
+    model = orc.OracleModel(w_cpu, max_seq_len=64, prefill="reference")
     setup = time.perf_counter() - t0
     log(f"cpu oracle ready ({setup:.0f} s)")
     prompt = synth.make_prompt(w_cpu.cfg, n=n_prompt, seed=7)

@@ -255,6 +255,39 @@ int qh_chain_sync_words(void);
 int qh_chain(const qh_chain_phase_t* phases, int nphase, unsigned* sync, int* err,
              qh_stream_t stream);
 
+/* ---- batch prefill pieces (the reference runs these in torch) ---------- */
+
+/* q/k head (1+w) RMSNorm + partial RoPE (q kept fp32, k cached bf16) and the
+ * KV-cache write for M tokens at positions past.. (replaces main.py:1034-1043). */
+int qh_attn_prep(const void* q_all, const void* k, const void* v, const float* q_norm_w,
+                 const float* k_norm_w, const float* cos_t, const float* sin_t, float* q_out,
+                 void* k_cache, void* v_cache, int M, int Hq, int Hkv, int D, int rot, int past,
+                 int max_seq, float eps, qh_stream_t stream);
+
+/* Causal GQA attention (fp32 softmax) with the bf16 sigmoid output gate for M
+ * query tokens (replaces main.py:1043-1059). */
+int qh_attn_prefill(const float* q, const void* gate, int gate_mstride, int gate_hstride,
+                    const void* k_cache, const void* v_cache, void* out, int M, int Hq, int Hkv,
+                    int D, int past, int max_seq, qh_stream_t stream);
+
+/* GatedDeltaNet prefill front: causal conv + SiLU over the sequence (conv ring
+ * updated), bf16-step l2norm of q/k, per-token gates (replaces
+ * main.py:1097-1128). */
+int qh_gdn_prep(const void* mixed, void* conv_ring, const void* conv_w, const void* a,
+                const void* b, const float* A_log, const float* dt_bias, void* y, void* qn,
+                void* kn, float* g, void* beta, int M, int Hk, int Hv, int dk, int dv, int past,
+                qh_stream_t stream);
+
+/* GatedDeltaNet prefill scan: recurrent gated delta rule from the stored
+ * state (updated in place) and the gated RMSNorm per token and head (replaces
+ * main.py:1139-1158, transformers torch_chunk_gated_delta_rule). */
+int qh_gdn_scan(const void* qn, const void* kn, const void* y, const float* g, const void* beta,
+                const void* z, const void* norm_w, float* state, void* out, int M, int Hk, int Hv,
+                int dk, int dv, float eps, qh_stream_t stream);
+
+/* m = bf16(bf16(silu(g)) * u), the M > 1 MLP glue (replaces main.py:1213-1215). */
+int qh_silu_mul(const void* g, const void* u, void* m, size_t n, qh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

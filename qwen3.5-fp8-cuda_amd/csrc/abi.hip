@@ -19,6 +19,7 @@
 #include "qh_attn.h"
 #include "qh_gdn.h"
 #include "qh_gemm.h"
+#include "qh_prefill.h"
 #include "qh_kernels.h"
 #include "qh_norm.h"
 
@@ -619,4 +620,65 @@ QH_EXPORT int qh_chain(const void* phases, int nphase, unsigned* sync, int* err,
                        hipStream_t stream) {
   if (qh_launch_chain((const QhChainPhaseDesc*)phases, nphase, sync, err, stream) != 0) return -1;
   return check_launch("qh_chain");
+}
+
+// ---- batch prefill pieces (the reference runs these in torch) -------------------
+// q/k head norm + partial RoPE (q kept fp32) + KV-cache write for M tokens at
+// positions past.. (main.py:1034-1043).
+QH_EXPORT int qh_attn_prep(const void* q_all, const void* k, const void* v, const float* q_norm_w,
+                           const float* k_norm_w, const float* cos_t, const float* sin_t,
+                           float* q_out, void* k_cache, void* v_cache, int M, int Hq, int Hkv,
+                           int D, int rot, int past, int max_seq, float eps, hipStream_t stream) {
+  QhAttnPrepParams p = {(const uint16_t*)q_all, (const uint16_t*)k, (const uint16_t*)v, q_norm_w,
+                        k_norm_w, cos_t, sin_t, q_out, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                        M, Hq, Hkv, D, rot, past, max_seq, eps};
+  if (qh_launch_attn_prep(p, stream) != 0) return -1;
+  return check_launch("qh_attn_prep");
+}
+
+// Causal GQA attention with the sigmoid output gate for M query tokens
+// (main.py:1043-1059).
+QH_EXPORT int qh_attn_prefill(const float* q, const void* gate, int gate_mstride, int gate_hstride,
+                              const void* k_cache, const void* v_cache, void* out, int M, int Hq,
+                              int Hkv, int D, int past, int max_seq, hipStream_t stream) {
+  QhAttnPrefillParams p = {q, (const uint16_t*)gate, gate_mstride, gate_hstride,
+                           (const uint16_t*)k_cache, (const uint16_t*)v_cache, (uint16_t*)out,
+                           M, Hq, Hkv, D, past, max_seq};
+  if (qh_launch_attn_prefill(p, stream) != 0) return -1;
+  return check_launch("qh_attn_prefill");
+}
+
+// GatedDeltaNet prefill front: causal conv + SiLU over the sequence (conv
+// ring updated), bf16-step l2norm of q/k, per-token gates (main.py:1097-1128).
+QH_EXPORT int qh_gdn_prep(const void* mixed, void* conv_ring, const void* conv_w, const void* a,
+                          const void* b, const float* A_log, const float* dt_bias, void* y, void* qn,
+                          void* kn, float* g, void* beta, int M, int Hk, int Hv, int dk, int dv,
+                          int past, hipStream_t stream) {
+  QhGdnPrepParams p = {(const uint16_t*)mixed, (uint16_t*)conv_ring, (const uint16_t*)conv_w,
+                       (const uint16_t*)a, (const uint16_t*)b, A_log, dt_bias, (uint16_t*)y,
+                       (uint16_t*)qn, (uint16_t*)kn, g, (uint16_t*)beta, M,
+                       2 * Hk * dk + Hv * dv, Hk, Hv, dk, dv, past};
+  if (qh_launch_gdn_prep(p, stream) != 0) return -1;
+  return check_launch("qh_gdn_prep");
+}
+
+// GatedDeltaNet prefill scan: recurrent gated delta rule over the M tokens from
+// the stored state (updated in place), gated RMSNorm per token and head
+// (main.py:1139-1158).
+QH_EXPORT int qh_gdn_scan(const void* qn, const void* kn, const void* y, const float* g,
+                          const void* beta, const void* z, const void* norm_w, float* state,
+                          void* out, int M, int Hk, int Hv, int dk, int dv, float eps,
+                          hipStream_t stream) {
+  QhGdnScanParams p = {(const uint16_t*)qn, (const uint16_t*)kn, (const uint16_t*)y, g,
+                       (const uint16_t*)beta, (const uint16_t*)z, (const uint16_t*)norm_w, state,
+                       (uint16_t*)out, M, 2 * Hk * dk + Hv * dv, Hk, Hv, dk, dv, eps};
+  if (qh_launch_gdn_scan(p, stream) != 0) return -1;
+  return check_launch("qh_gdn_scan");
+}
+
+// m = bf16(bf16(silu(g)) * u), the M > 1 MLP glue (main.py:1213-1215).
+QH_EXPORT int qh_silu_mul(const void* g, const void* u, void* m, size_t n, hipStream_t stream) {
+  if (qh_launch_silu_mul((const uint16_t*)g, (const uint16_t*)u, (uint16_t*)m, n, stream) != 0)
+    return -1;
+  return check_launch("qh_silu_mul");
 }

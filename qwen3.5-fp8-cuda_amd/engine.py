@@ -50,7 +50,7 @@ def default_attn_splits(max_seq):
 
 class Qwen35FP8Engine:
     def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda",
-                 use_chain=False):
+                 use_chain=False, batch_prefill=True):
         if not torch.cuda.is_available():
             raise RuntimeError("Qwen35FP8Engine needs a GPU (there is no CPU fallback)")
         self.lib = abi.load()
@@ -106,6 +106,8 @@ class Qwen35FP8Engine:
                                               device=dev))
         self.graph = None
         self.prompt_buf = None
+        self.batch_prefill = batch_prefill
+        self._pf = None          # prefill buffers, sized for the longest prompt seen
         # Chained launches (qh_chain): per layer, the mixer's output projection,
         # gate/up, down and the next layer's input projection run as one launch.
         self.use_chain = use_chain and self._chain_shapes_ok()
@@ -302,6 +304,8 @@ class Qwen35FP8Engine:
                              f"max_seq_len={self.max_seq_len}")
         if logits_to_keep != 1:
             raise ValueError("only logits_to_keep=1 is supported")
+        if s > 1 and past_len == 0 and self.batch_prefill:
+            return self.prefill_batch(ids)
         st = abi.stream_handle()
         self.pos.fill_(past_len)
         for t in range(s):
@@ -315,6 +319,119 @@ class Qwen35FP8Engine:
         """Run the prompt; afterwards tok holds the greedy next token, h its
         embedding and pos = len(ids)."""
         self.forward(ids, past_len=0)
+
+    # --------------------------------------------------------- batch prefill
+    def _prefill_buffers(self, M):
+        if self._pf is not None and self._pf["M"] >= M:
+            return self._pf
+        cfg, dev = self.cfg, self.device
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        kmax = max(H, I, cfg.attn_out_dim, cfg.value_dim)
+        ws = int(self.lib.qh_gemm_workspace_size(M, kmax))
+        self._pf = {
+            "M": M, "h": torch.empty(M, H, **bf), "hn": torch.empty(M, H, **bf),
+            "o": torch.empty(M, H, **bf), "q_all": torch.empty(M, cfg.q_proj_rows, **bf),
+            "k": torch.empty(M, cfg.kv_rows, **bf), "v": torch.empty(M, cfg.kv_rows, **bf),
+            "q32": torch.empty(M, cfg.num_attention_heads * cfg.head_dim, dtype=torch.float32,
+                               device=dev),
+            "att": torch.empty(M, cfg.attn_out_dim, **bf),
+            "mixed": torch.empty(M, cfg.conv_dim, **bf), "y": torch.empty(M, cfg.conv_dim, **bf),
+            "z": torch.empty(M, cfg.value_dim, **bf),
+            "a": torch.empty(M, cfg.linear_num_value_heads, **bf),
+            "b": torch.empty(M, cfg.linear_num_value_heads, **bf),
+            "qn": torch.empty(M, cfg.key_dim, **bf), "kn": torch.empty(M, cfg.key_dim, **bf),
+            "g": torch.empty(M, cfg.linear_num_value_heads, dtype=torch.float32, device=dev),
+            "beta": torch.empty(M, cfg.linear_num_value_heads, **bf),
+            "gated": torch.empty(M, cfg.value_dim, **bf),
+            "gu_g": torch.empty(M, I, **bf), "gu_u": torch.empty(M, I, **bf),
+            "m": torch.empty(M, I, **bf), "ids": torch.empty(M, dtype=torch.int64, device=dev),
+            "ws": torch.empty(max(ws, 16), dtype=torch.uint8, device=dev),
+        }
+        return self._pf
+
+    def _gemm(self, x, ws_pair, y, M, ws):
+        w, s = ws_pair
+        abi.check(self.lib.qh_gemm_e4m3(abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M,
+                                        w.shape[0], w.shape[1], ops.scale_mode(w, s),
+                                        int(s.dtype == torch.bfloat16), abi.ptr(ws),
+                                        abi.stream_handle()), "gemm")
+
+    def prefill_batch(self, ids):
+        """The reference's s > 1 prefill (main.py:1550-1566) for a prompt at
+        position 0: every projection as an FP8 GEMM over the M tokens, batch
+        attention / GatedDeltaNet kernels, then the lm_head + greedy argmax of
+        the last token.  Afterwards tok holds the next token, h its embedding
+        and pos = M (the recurrent state continues from the prompt)."""
+        cfg, L = self.cfg, self.lib
+        ids = ids.reshape(-1).to(self.device, torch.int64)
+        M = ids.numel()
+        if M < 1 or M > self.max_seq_len:
+            raise ValueError(f"prompt of {M} tokens does not fit max_seq_len={self.max_seq_len}")
+        B = self._prefill_buffers(M)
+        st = abi.stream_handle()
+        H, I, eps = cfg.hidden_size, cfg.intermediate_size, self.eps
+        self._reset_cache()
+        h, hn, o, ws = B["h"][:M], B["hn"][:M], B["o"][:M], B["ws"]
+        B["ids"][:M].copy_(ids)
+        abi.check(L.qh_embed(abi.ptr(self.w.embed), abi.ptr(B["ids"]), abi.ptr(h), M, H,
+                             cfg.vocab_size, st), "embed")
+        for i in range(cfg.num_hidden_layers):
+            ly = self.w.layers[i]
+            abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(ly["input_layernorm"]), abi.ptr(hn), M, H,
+                                   eps, st), "rmsnorm")
+            if cfg.is_full(i):
+                D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
+                q_all, k, v = B["q_all"][:M], B["k"][:M], B["v"][:M]
+                self._gemm(hn, ly["q_proj"], q_all, M, ws)
+                self._gemm(hn, ly["k_proj"], k, M, ws)
+                self._gemm(hn, ly["v_proj"], v, M, ws)
+                abi.check(L.qh_attn_prep(abi.ptr(q_all), abi.ptr(k), abi.ptr(v),
+                                         abi.ptr(ly["q_norm"]), abi.ptr(ly["k_norm"]),
+                                         abi.ptr(self.rope_cos), abi.ptr(self.rope_sin),
+                                         abi.ptr(B["q32"]), abi.ptr(self.k_cache[i]),
+                                         abi.ptr(self.v_cache[i]), M, Hq, Hkv, D, cfg.rotary_dim, 0,
+                                         self.max_seq_len, eps, st), "attn_prep")
+                abi.check(L.qh_attn_prefill(abi.ptr(B["q32"]), abi.ptr(q_all[:, D:]), Hq * 2 * D,
+                                            2 * D, abi.ptr(self.k_cache[i]),
+                                            abi.ptr(self.v_cache[i]), abi.ptr(B["att"]), M, Hq, Hkv,
+                                            D, 0, self.max_seq_len, st), "attn_prefill")
+                self._gemm(B["att"][:M], ly["o_proj"], o, M, ws)
+            else:
+                Hk, Hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+                dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+                self._gemm(hn, ly["in_proj_qkv"], B["mixed"][:M], M, ws)
+                self._gemm(hn, ly["in_proj_z"], B["z"][:M], M, ws)
+                self._gemm(hn, ly["in_proj_b"], B["b"][:M], M, ws)
+                self._gemm(hn, ly["in_proj_a"], B["a"][:M], M, ws)
+                abi.check(L.qh_gdn_prep(abi.ptr(B["mixed"]), abi.ptr(self.conv_ring[i]),
+                                        abi.ptr(ly["conv1d_w"]), abi.ptr(B["a"]), abi.ptr(B["b"]),
+                                        abi.ptr(ly["A_log"]), abi.ptr(ly["dt_bias"]),
+                                        abi.ptr(B["y"]), abi.ptr(B["qn"]), abi.ptr(B["kn"]),
+                                        abi.ptr(B["g"]), abi.ptr(B["beta"]), M, Hk, Hv, dk, dv, 0,
+                                        st), "gdn_prep")
+                abi.check(L.qh_gdn_scan(abi.ptr(B["qn"]), abi.ptr(B["kn"]), abi.ptr(B["y"]),
+                                        abi.ptr(B["g"]), abi.ptr(B["beta"]), abi.ptr(B["z"]),
+                                        abi.ptr(ly["norm_w"]), abi.ptr(self.state[i]),
+                                        abi.ptr(B["gated"]), M, Hk, Hv, dk, dv, 1e-6, st),
+                          "gdn_scan")
+                self._gemm(B["gated"][:M], ly["out_proj"], o, M, ws)
+            abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
+            abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(ly["post_attention_layernorm"]),
+                                   abi.ptr(hn), M, H, eps, st), "rmsnorm")
+            self._gemm(hn, ly["gate_proj"], B["gu_g"][:M], M, ws)
+            self._gemm(hn, ly["up_proj"], B["gu_u"][:M], M, ws)
+            abi.check(L.qh_silu_mul(abi.ptr(B["gu_g"]), abi.ptr(B["gu_u"]), abi.ptr(B["m"]), M * I,
+                                    st), "silu_mul")
+            self._gemm(B["m"][:M], ly["down_proj"], o, M, ws)
+            abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
+        self.pos.fill_(M - 1)
+        abi.check(L.qh_lm_head_argmax(
+            abi.ptr(h[M - 1]), abi.ptr(self.w.norm_f), eps, H, abi.ptr(self.w.lm_head),
+            cfg.vocab_size, abi.ptr(self.logits), abi.ptr(self.lm_scratch),
+            abi.ptr(self.lm_counter), abi.ptr(self.tok), abi.ptr(self.tok_hist), self.max_seq_len,
+            abi.ptr(self.pos), abi.ptr(self.w.embed), abi.ptr(self.h), st), "lm_head_argmax")
+        return self.logits.view(1, -1)
 
     def generate(self, n_steps):
         """n greedy steps from the current device state (no host sync)."""

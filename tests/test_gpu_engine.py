@@ -15,7 +15,9 @@ pytestmark = pytest.mark.gpu
 def _run(cfg, n_prompt, n_steps, graph):
     w = make_weights(cfg, seed=0)
     prompt = make_prompt(cfg, n=n_prompt, seed=1)
-    eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=128)
+    # the prompt runs through the decode path here (sequential prefill), so
+    # that every position is checked against the oracle's decode path
+    eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=128, batch_prefill=False)
     if graph:
         eng.capture()
     eng._reset_cache()
