@@ -97,3 +97,20 @@ def test_chained_launches_equal_separate_launches(graph):
     assert torch.equal(f1, f2)
     assert t1 == t2
     assert torch.equal(l1, l2)
+
+
+def test_engine_on_loaded_checkpoint_bf16_scales(tmp_path):
+    """A checkpoint written in the released layout, loaded like the reference
+    loads it (scale_inv rounded to bf16), decodes like the oracle on the same
+    loaded weights."""
+    from qwen35_amd import loader
+    cfg = tiny(num_layers=4)
+    loader.save_checkpoint(make_weights(cfg, seed=9), str(tmp_path))
+    w = loader.load_checkpoint(str(tmp_path), device="cpu")
+    assert w.layers[0]["gate_proj"][1].dtype == torch.bfloat16
+    prompt = make_prompt(cfg, n=7, seed=2)
+    eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=64)
+    logits = eng.forward(prompt.view(1, -1).cuda(), 0).float().cpu().view(-1)
+    ref = orc.OracleModel(w, max_seq_len=64, prefill="reference")
+    rl = ref.forward(prompt.view(1, -1), 0).view(-1)
+    assert cos_sim(logits, rl) > 0.9999
