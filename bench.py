@@ -50,14 +50,20 @@ def mlp_bytes(cfg):
     return w + s + H * 2 + H * 4 + I * 2           # + x, norm weights, output
 
 
+# The gate/up kernel the decode step launches (name as rocprofv3 reports it).
+GATE_UP_KERNEL = "mlp_fast_kernel<5, 1, float>(QhMlpParams)"
+
+
 def measured_traffic():
     """HBM bytes per gate/up launch from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each calibrated on a copy of known size), or None
-    when there is none."""
+    when there is none for the kernel the library launches now."""
     path = os.path.join(ROOT, "profiles", "gate_up_traffic_pmc.json")
     try:
         with open(path) as f:
             d = json.load(f)
+        if d["kernel"] != GATE_UP_KERNEL:
+            return None, None
         return int(d["traffic_bytes_per_launch"]), d["kernel"]
     except (OSError, KeyError, ValueError):
         return None, None
@@ -273,8 +279,8 @@ def main():
             "baseline": "reference README 53.9 tok/s on RTX 5060 (different GPU, real checkpoint)",
         },
         "roofline": {
-            "kernel": "mlp_fast_kernel<5, 2, float> (fused RMSNorm + gate/up E4M3 GEMV + "
-                      "SiLU*up), 9216x2560 x2",
+            "kernel": GATE_UP_KERNEL + " (fused RMSNorm + gate/up E4M3 GEMV + SiLU*up), "
+                      "9216x2560 x2",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -253,6 +253,15 @@ struct XSlice {
   __device__ __forceinline__ u32x4 operator[](int j) const { return XLDS ? get_lds(j) : r[XLDS ? 0 : j]; }
 };
 
+// The fast path's register slice (K == 512 * CPL): chunk j of lane l is
+// x[8c, 8c + 8) with c = l + 64 j, read once from the staged activation.
+template <int CPL>
+__device__ __forceinline__ void x_slice(u32x4 (&xr)[CPL], const uint16_t* sx) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) xr[j] = *(const u32x4*)(sx + (lane + 64 * j) * 8);
+}
+
 template <int CPL>
 __device__ __forceinline__ void block_x_prologue(u32x4 (&xr)[CPL], uint16_t* sx, float* red,
                                                  const uint16_t* x, const uint16_t* x2,
@@ -556,9 +565,9 @@ __device__ __forceinline__ void issue_fast(u32x2 (&w)[CPL], float (&sr_)[scale_r
   }
 }
 
-template <int CPL, bool XLDS>
+template <int CPL>
 __device__ __forceinline__ float dot_row(const u32x2 (&w)[CPL], const float (&sr_)[scale_regs<CPL>()],
-                                         const XSlice<CPL, XLDS>& xs, uint32_t q4) {
+                                         const u32x4 (&xs)[CPL], uint32_t q4) {
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -569,6 +578,26 @@ __device__ __forceinline__ float dot_row(const u32x2 (&w)[CPL], const float (&sr
     acc = fmaf(dot8_e4m3_bf16(w[j].x, w[j].y, xs[j], 0.0f), sc, acc);
   }
   return acc;
+}
+
+// Fast-path pipeline shape per K (measured on MI355X at the decode shapes):
+//   fast_depth: row groups a wave keeps in flight;
+//   fast_lead: row groups issued before the wave waits for its activation.
+// A launch puts ~20 MB of weight requests in flight at once, and at that queue
+// depth every request -- the activation's included, although it is issued
+// first -- takes ~3.5 us to return.  Waiting for the activation before most of
+// the weight stream is issued lets the first dot products start as soon as
+// the first rows land.
+constexpr int fast_depth(int cpl) { return cpl <= 6 ? 4 : 1; }
+constexpr int fast_lead(int cpl) { return cpl <= 6 ? 1 : 0; }
+constexpr int mlp_fast_depth(int) { return 1; }
+constexpr int mlp_fast_lead(int) { return 0; }
+
+// Holds the wave until its first activation chunk (and every load issued
+// before it) has arrived.
+template <int CPL, int NT>
+__device__ __forceinline__ void x_arrived(const XIn<CPL, NT>& in) {
+  asm volatile("; activation %0" ::"v"(in.v[0].x) : "memory");
 }
 
 // Dependency of a chained phase: wait until *done >= need.  Thread 0 polls
@@ -620,12 +649,14 @@ __device__ __forceinline__ void chain_wait(const QhWait& w) {
 }
 
 // Grouped E4M3 GEMV, one phase's share: workgroup `wg` of `nwg`.
-// CH = false: standalone launch; the activation loads go out first (K <= 4096),
-//   then the weight pipeline.
+// CH = false: standalone launch; the activation loads go out first, then the
+//   weight pipeline.
 // CH = true: a dependent phase of the chained kernel; the weight pipeline
 //   (which does not depend on earlier phases) goes out first, then the wait,
 //   then the activation and residual loads (coherent).
 // OUTC: outputs stored coherently (read by later phases of the same launch).
+// NORM: the (1+w) RMSNorm prologue may be requested (p.norm_w); without it the
+//   norm weights take no registers.
 template <int CPL, int P, typename ScaleT, bool CH, bool OUTC = CH, int NT = 256>
 __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, int nwg, uint16_t* sx,
                                                float* red, const QhWait& wt) {
@@ -664,30 +695,28 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
   (void)res;
 
   XIn<CPL, NT> xin;
-  if (!CH && early_x<CPL>()) block_x_load<CPL, CH, NT>(xin, p.x, p.x2, p.norm_w, K);
+  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K);
 #pragma unroll
   for (int s = 0; s < P; ++s) {
+    if (!CH && s == fast_lead(CPL)) x_arrived(xin);
     issue_w(w[s], sc[s], srow[s], sseg[s], g + s * stride);
     if (!CH) issue_res(res[s], srow[s], g + s * stride);
   }
   if (CH) {
     chain_wait(wt);
-    if (early_x<CPL>()) block_x_load<CPL, CH, NT>(xin, p.x, p.x2, p.norm_w, K);
+    block_x_load<CPL, true, NT>(xin, p.x, p.x2, p.norm_w, K);
 #pragma unroll
     for (int s = 0; s < P; ++s) issue_res(res[s], srow[s], g + s * stride);
   }
-  if (early_x<CPL>())
-    block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
-  else
-    block_x_direct<CPL, CH, NT>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
-  XSlice<CPL, (CPL > 8)> xs;
-  xs.init(sx, K);
+  u32x4 xr[CPL];
+  block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  x_slice<CPL>(xr, sx);
 
   for (;;) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       if (g >= p.gtotal) return;
-      const float acc = wave_total(dot_row<CPL>(w[s], sc[s], xs, q4));
+      const float acc = wave_total(dot_row<CPL>(w[s], sc[s], xr, q4));
       if (lane == 0) {
         float y = rbf(acc);
         if (p.res1) y = res[s] + y;
@@ -714,32 +743,30 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
   int g = wg * NW + wid;
 
   XIn<CPL, NT> xin;
-  if (!CH && early_x<CPL>()) block_x_load<CPL, CH, NT>(xin, p.x, p.x2, p.norm_w, K);
+  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K);
   u32x2 wg_[P][CPL], wu[P][CPL];
   float sg[P][scale_regs<CPL>()], su[P][scale_regs<CPL>()];
 #pragma unroll
   for (int s = 0; s < P; ++s) {
+    if (!CH && s == mlp_fast_lead(CPL)) x_arrived(xin);
     const int gg = g + s * stride;
     issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gg, gg < p.N, lw, lane);
     issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gg, gg < p.N, lw, lane);
   }
   if (CH) {
     chain_wait(wt);
-    if (early_x<CPL>()) block_x_load<CPL, CH, NT>(xin, p.x, p.x2, p.norm_w, K);
+    block_x_load<CPL, true, NT>(xin, p.x, p.x2, p.norm_w, K);
   }
-  if (early_x<CPL>())
-    block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
-  else
-    block_x_direct<CPL, CH, NT>(sx, red, p.x, p.x2, p.norm_w, p.eps, K);
-  XSlice<CPL, (CPL > 8)> xs;
-  xs.init(sx, K);
+  u32x4 xr[CPL];
+  block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  x_slice<CPL>(xr, sx);
 
   for (;;) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       if (g >= p.N) return;
-      const float ag = wave_total(dot_row<CPL>(wg_[s], sg[s], xs, q4));
-      const float au = wave_total(dot_row<CPL>(wu[s], su[s], xs, q4));
+      const float ag = wave_total(dot_row<CPL>(wg_[s], sg[s], xr, q4));
+      const float au = wave_total(dot_row<CPL>(wu[s], su[s], xr, q4));
       if (lane == 0) {
         // SiLU on the fp32 accumulators (fused_kernels.cu:476).
         st_act1<OUTC>(p.m_out + g, f2bf(qh_silu(ag) * au));
@@ -754,9 +781,13 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
   }
 }
 
+// Standalone fast kernels.
+// The launchers run two workgroups per CU, i.e. two waves per SIMD, so that is
+// the occupancy asked of the compiler (the register budget then holds the
+// activation slice, the norm weights and the P-deep weight pipeline unspilled).
 template <int CPL, int P, typename ScaleT, int NT = 256>
 __global__ __launch_bounds__(NT)
-__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void gemv_fast_kernel(QhGemvParams p) {
+__attribute__((amdgpu_waves_per_eu(2))) void gemv_fast_kernel(QhGemvParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[NT / 64];
   const QhWait none = {nullptr, 0ull, nullptr};
@@ -765,7 +796,7 @@ __attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void gemv_fast_kernel(
 
 template <int CPL, int P, typename ScaleT, int NT = 256>
 __global__ __launch_bounds__(NT)
-__attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void mlp_fast_kernel(QhMlpParams p) {
+__attribute__((amdgpu_waves_per_eu(2))) void mlp_fast_kernel(QhMlpParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[NT / 64];
   const QhWait none = {nullptr, 0ull, nullptr};
@@ -805,14 +836,12 @@ struct QhChainParams {
   int* err;  // set to 1 if a wait expired
 };
 
-constexpr int kChainMaxCpl = 18;
-
 __device__ __forceinline__ unsigned* chain_phase_parts(unsigned* sync, int k) {
   return sync + kChainPartStride * kChainParts * k;
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void chain_kernel(QhChainParams c) {
-  __shared__ __align__(16) uint16_t sx[kChainMaxCpl * 512];
+  __shared__ __align__(16) uint16_t sx[18 * 512];
   __shared__ float red[4];
   __shared__ unsigned long long s_epoch;
   const int wg = blockIdx.x, nwg = gridDim.x;
@@ -821,7 +850,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
       const unsigned long long n = chain_count(chain_phase_parts(c.sync, c.nphase - 1));
       if (threadIdx.x == 0) s_epoch = n / (unsigned)nwg;
     }
-    // (the barrier inside the first body's prologue publishes s_epoch)
+    __syncthreads();
   }
 #pragma unroll
   for (int k = 0; k < kChainMaxPhases; ++k) {
@@ -980,16 +1009,10 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
 }
 
 // ---- launchers ----------------------------------------------------------------
-// Row-group size R and pipeline depth P per chunks-per-lane class (measured on
-// MI355X at the decode shapes: many waves with a few rows each, every wave of
-// the grid resident at once, two groups in flight per wave).
-// Generic kernels (any scale mode, any K % 8 == 0): one row, one group in
-// flight.  Fast kernels: two rows in flight per wave while the activation
-// slice lives in registers (K <= 4096), one above.
+// Generic kernels (any scale mode, any K % 8 == 0): row-group size R and
+// pipeline depth P per chunks-per-lane class: one row, one group in flight.
 constexpr int gemv_rows(int cpl) { return cpl > 0 ? 1 : 1; }
 constexpr int gemv_depth(int cpl) { return cpl > 0 ? 1 : 1; }
-constexpr int fast_depth(int cpl) { return cpl <= 6 ? 4 : 1; }
-constexpr int mlp_fast_depth(int cpl) { return cpl <= 6 ? 2 : 1; }
 constexpr uint32_t kMaxBufferBytes = 0x7fffffffu;
 
 int cu_count() {
@@ -1043,7 +1066,7 @@ void launch_mlp_t(const QhMlpParams& p, hipStream_t st) {
 template <int CPL, typename ScaleT>
 void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
   // Two workgroups per CU, each wave walking several rows, measured faster than
-  // filling every slot (fewer activation prologues, same bytes in flight).
+  // filling every slot.
   auto fn = gemv_fast_kernel<CPL, fast_depth(CPL), ScaleT>;
   const int grid = std::max(1, std::min({resident_blocks((const void*)fn), 2 * cu_count(), (p.gtotal + 3) / 4}));
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
