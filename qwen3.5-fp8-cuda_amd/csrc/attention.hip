@@ -67,9 +67,11 @@ __device__ __forceinline__ void store_head_f32_coherent(float* head, int lane, c
   }
 }
 template <int NPL>
-__device__ __forceinline__ void load_head_f32_coherent(float (&v)[NPL], const float* head, int lane) {
+__device__ __forceinline__ void load_head_f32_coherent(float (&v)[NPL], const float* head, int lane,
+                                                       bool valid = true) {
+  // valid == false: a zero-range resource, the load returns zeros untouched
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(head), (short)0, (int)(64 * NPL * 4), 0x00020000);
+      const_cast<float*>(head), (short)0, valid ? (int)(64 * NPL * 4) : 0, 0x00020000);
   const uint32_t off = (uint32_t)lane * NPL * 4u;
   if constexpr (NPL == 4) {
     const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
@@ -81,21 +83,51 @@ __device__ __forceinline__ void load_head_f32_coherent(float (&v)[NPL], const fl
   }
 }
 
+// Per-lane operands of the head norm and RoPE: lane l holds dims
+// c = l * NPL + i.  They are loaded once, up front, so the norm and rotation
+// below never wait on memory.
+template <int NPL>
+struct NormRopeIn {
+  float qw[NPL], kw[NPL];  // (1+w) norm weights of q and k (w)
+  float cs[NPL], sn[NPL];  // cos / sin of dim c at the position (c < rot)
+};
+
+template <int NPL>
+__device__ __forceinline__ void load_norm_w(NormRopeIn<NPL>& in, const float* q_norm_w,
+                                            const float* k_norm_w, int lane) {
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane * NPL + i;
+    in.qw[i] = q_norm_w ? q_norm_w[c] : 0.0f;
+    in.kw[i] = k_norm_w ? k_norm_w[c] : 0.0f;
+  }
+}
+template <int NPL>
+__device__ __forceinline__ void load_rope(NormRopeIn<NPL>& in, const float* cos_row, const float* sin_row,
+                                          int rot, int lane) {
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int c = lane * NPL + i;
+    const int cr = c < rot ? c : 0;
+    in.cs[i] = rot > 0 ? cos_row[cr] : 1.0f;
+    in.sn[i] = rot > 0 ? sin_row[cr] : 0.0f;
+  }
+}
+
 // bf16 (1+w) RMSNorm over a D-wide head held NPL values per lane, then bf16
 // partial RoPE.  All lanes of the wave must call this.
 template <int D>
-__device__ __forceinline__ void norm_rope(float (&v)[D / 64], const float* norm_w, float eps,
-                                          const float* cos_row, const float* sin_row, int rot,
-                                          int lane) {
+__device__ __forceinline__ void norm_rope(float (&v)[D / 64], bool has_norm, const float (&nw)[D / 64],
+                                          const NormRopeIn<D / 64>& r, float eps, int rot, int lane) {
   constexpr int NPL = D / 64;
-  if (norm_w) {
+  if (has_norm) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) ss = fmaf(v[i], v[i], ss);
     ss = wave_sum(ss);
-    const float r = rsqrtf(ss / (float)D + eps);
+    const float rs = rsqrtf(ss / (float)D + eps);
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) v[i] = rbf(v[i] * r * (1.0f + norm_w[lane * NPL + i]));
+    for (int i = 0; i < NPL; ++i) v[i] = rbf(v[i] * rs * (1.0f + nw[i]));
   }
   if (rot > 0) {
     const int half = rot >> 1;
@@ -104,11 +136,9 @@ __device__ __forceinline__ void norm_rope(float (&v)[D / 64], const float* norm_
     for (int i = 0; i < NPL; ++i) {
       const float partner = __shfl_xor(v[i], pm, 64);
       const int c = lane * NPL + i;
-      if (c < half) {
-        v[i] = rbf(v[i] * cos_row[c] - partner * sin_row[c]);
-      } else if (c < rot) {
-        v[i] = rbf(v[i] * cos_row[c] + partner * sin_row[c]);
-      }
+      const float lo = v[i] * r.cs[i] - partner * r.sn[i];   // c < rot/2
+      const float hi = v[i] * r.cs[i] + partner * r.sn[i];   // rot/2 <= c < rot
+      v[i] = c < half ? rbf(lo) : (c < rot ? rbf(hi) : v[i]);
     }
   }
 }
@@ -129,8 +159,29 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   const int kvh = blockIdx.x;
   const int split = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  // wave-uniform (scalar) so per-head buffer resources need no waterfall loop
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = p.n_heads / p.n_kv;
+
+  // Loads that do not depend on the position go out first: this wave's query
+  // heads and output gates, the new token's K/V (wave 0) and the norm weights.
+  float qraw[HPW][NPL], gate_v[HPW][NPL];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi;
+    if (gi < G) {
+      load_head<NPL>(qraw[hi], p.q + (size_t)(kvh * G + gi) * p.q_stride + lane * NPL);
+      if (p.gate)
+        load_head<NPL>(gate_v[hi], p.gate + (size_t)(kvh * G + gi) * p.gate_stride + lane * NPL);
+    }
+  }
+  float kraw[NPL], vraw[NPL];
+  if (wid == 0 && p.k_new) {
+    load_head<NPL>(kraw, p.k_new + (size_t)kvh * D + lane * NPL);
+    load_head<NPL>(vraw, p.v_new + (size_t)kvh * D + lane * NPL);
+  }
+  NormRopeIn<NPL> nr;
+  load_norm_w<NPL>(nr, p.q_norm_w, p.k_norm_w, lane);
 
   int rope_pos = p.rope_pos, slot = p.slot, total = p.total;
   if (p.pos_dev) {
@@ -195,32 +246,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     }
   };
   if (p0 < p1) fetch(p0);
+  load_rope<NPL>(nr, cos_row, sin_row, p.rot, lane);
 
-  // Output gate values of this wave's heads, loaded now (they are needed only
-  // by the workgroup that emits, after the merge).
-  float gate_v[HPW][NPL];
+  // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
     const int gi = wid + 4 * hi;
-    if (p.gate && gi < G)
-      load_head<NPL>(gate_v[hi], p.gate + (size_t)(kvh * G + gi) * p.gate_stride + lane * NPL);
-  }
-
-  // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
-  for (int gi = wid; gi < G; gi += 4) {
+    if (gi >= G) continue;
     const int h = kvh * G + gi;
-    float qv[NPL];
-    load_head<NPL>(qv, p.q + (size_t)h * p.q_stride + lane * NPL);
-    norm_rope<D>(qv, p.q_norm_w, p.eps, cos_row, sin_row, p.rot, lane);
-    store_head<NPL>(sQ + gi * D + lane * NPL, qv);
-    if (p.q_wb && split == 0) store_head<NPL>(p.q_wb + (size_t)h * D + lane * NPL, qv);
+    norm_rope<D>(qraw[hi], p.q_norm_w != nullptr, nr.qw, nr, p.eps, p.rot, lane);
+    store_head<NPL>(sQ + gi * D + lane * NPL, qraw[hi]);
+    if (p.q_wb && split == 0) store_head<NPL>(p.q_wb + (size_t)h * D + lane * NPL, qraw[hi]);
   }
   // ---- the new token's K (norm + RoPE) and V -------------------------------
   if (wid == 0 && p.k_new) {
-    float kv[NPL], vv[NPL];
-    load_head<NPL>(kv, p.k_new + (size_t)kvh * D + lane * NPL);
-    load_head<NPL>(vv, p.v_new + (size_t)kvh * D + lane * NPL);
-    norm_rope<D>(kv, p.k_norm_w, p.eps, cos_row, sin_row, p.rot, lane);
+    float (&kv)[NPL] = kraw;
+    float (&vv)[NPL] = vraw;
+    norm_rope<D>(kv, p.k_norm_w != nullptr, nr.kw, nr, p.eps, p.rot, lane);
     store_head<NPL>(sKn + lane * NPL, kv);
     store_head<NPL>(sVn + lane * NPL, vv);
     if (owner) {
@@ -341,19 +383,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     const bool have = lane < nactive;
     const float ls = have ? pub_load(base + lane * sstride + D + 1) : 0.0f;
     const float ms = have ? pub_load(base + lane * sstride + D) : -INFINITY;
+    // The partials of MB splits are requested together (one memory round trip
+    // per batch, not per split; the first batch travels with the (m, l)
+    // loads); slots past the last active split load zeros.
+    constexpr int MB = 8;
+    float part[MB][NPL];
+#pragma unroll
+    for (int u = 0; u < MB; ++u)
+      load_head_f32_coherent<NPL>(part[u], base + (size_t)u * sstride, lane, u < nactive);
     const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
     const float ws = ls > 0.0f ? __expf(ms - M) : 0.0f;
     const float L = wave_sum(ls * ws);
     float acc[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
-    for (int s = 0; s < nactive; ++s) {
-      const float w = __shfl(ws, s, 64);
-      if (w == 0.0f) continue;  // uniform: empty split
-      float part[NPL];
-      load_head_f32_coherent<NPL>(part, base + s * sstride, lane);
+    for (int s0 = 0; s0 < nactive; s0 += MB) {
+      if (s0 > 0) {
 #pragma unroll
-      for (int i = 0; i < NPL; ++i) acc[i] = fmaf(part[i], w, acc[i]);
+        for (int u = 0; u < MB; ++u)
+          load_head_f32_coherent<NPL>(part[u], base + (size_t)(s0 + u) * sstride, lane, s0 + u < nactive);
+      }
+#pragma unroll
+      for (int u = 0; u < MB; ++u) {
+        const float w = __shfl(ws, s0 + u, 64);  // s0 + u < 64: nsplit <= 64
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) acc[i] = w != 0.0f ? fmaf(part[u][i], w, acc[i]) : acc[i];
+      }
     }
     emit(gi, gate_v[hi], acc, 1.0f / L);
   }

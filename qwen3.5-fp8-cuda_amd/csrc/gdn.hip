@@ -107,21 +107,10 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
   const int rg = tid >> 7;
   const int lane = tid & 63, wid = tid >> 6;
 
-  // The state is the bulk of the traffic: request it first.
-  float* cols = p.state + (size_t)h * DK * DV + j;
-  float S[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) S[i] = cols[(size_t)(rg * RPT + i) * DV];
-  // Operands of the output norm, needed last, requested early.
-  float zv = 0.0f, nw = 0.0f;
-  if (rg == 0) {
-    zv = bf2f(p.z[(size_t)h * DV + j]);
-    nw = bf2f(p.norm_w[j]);
-  }
-
-  // ---- causal conv (window of 4) + SiLU: q/k of key head kh (threads
-  // 0..255), v of value head h (256..383) ------------------------------------
-  float y = 0.0f;
+  // Vector-memory loads complete in issue order, so the few small operands go
+  // out before the head's 64 KB of state: the conv, norms and gates then run
+  // while the state is still arriving.  The conv window is read as the whole
+  // 4-slot ring row (one 8-byte load, independent of the position).
   int c = -1;
   if (tid < 2 * DK) {
     const bool is_k = tid >= DK;
@@ -129,14 +118,36 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
   } else if (tid < 2 * DK + DV) {
     c = 2 * p.Hk * DK + h * DV + (tid - 2 * DK);
   }
+  uint16_t x_t = 0;
+  u32x2 ring4 = {0u, 0u}, w4 = {0u, 0u};
   if (c >= 0) {
-    const uint16_t x_t = p.mixed[c];
-    const uint16_t* ring = p.conv_ring + (size_t)c * 4;
-    const uint16_t* w = p.conv_w + (size_t)c * 4;
-    float acc = bf2f(w[3]) * bf2f(x_t);
-    acc = fmaf(bf2f(w[2]), bf2f(ring[(t + 3) & 3]), acc);
-    acc = fmaf(bf2f(w[1]), bf2f(ring[(t + 2) & 3]), acc);
-    acc = fmaf(bf2f(w[0]), bf2f(ring[(t + 1) & 3]), acc);
+    x_t = p.mixed[c];
+    ring4 = *(const u32x2*)(p.conv_ring + (size_t)c * 4);
+    w4 = *(const u32x2*)(p.conv_w + (size_t)c * 4);
+  }
+  const float bh = bf2f(p.b[h]), ah = bf2f(p.a[h]);
+  const float A_log = p.A_log[h], dt_bias = p.dt_bias[h];
+  // Operands of the output norm, needed last (loaded by every row group so
+  // no branch waits on them).
+  const uint16_t zraw = p.z[(size_t)h * DV + j], nwraw = p.norm_w[j];
+  float* cols = p.state + (size_t)h * DK * DV + j;
+  float S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) S[i] = cols[(size_t)(rg * RPT + i) * DV];
+
+  // ---- causal conv (window of 4) + SiLU: q/k of key head kh (threads
+  // 0..255), v of value head h (256..383) ------------------------------------
+  float y = 0.0f;
+  if (c >= 0) {
+    // slot s of the ring holds bf16 lane s of (ring4.x lo, hi, ring4.y lo, hi)
+    auto slot = [&](int sidx) {
+      const uint32_t wv = (sidx & 2) ? ring4.y : ring4.x;
+      return (sidx & 1) ? bf_hi(wv) : bf_lo(wv);
+    };
+    float acc = bf_hi(w4.y) * bf2f(x_t);
+    acc = fmaf(bf_lo(w4.y), slot((t + 3) & 3), acc);
+    acc = fmaf(bf_hi(w4.x), slot((t + 2) & 3), acc);
+    acc = fmaf(bf_lo(w4.x), slot((t + 1) & 3), acc);
     y = rbf(qh_silu(rbf(acc)));
     // q/k channels are shared by the r value heads of a key head: one writes.
     if (tid >= 2 * DK || (h % r) == 0) p.conv_ring[(size_t)c * 4 + (t & 3)] = x_t;
@@ -154,8 +165,8 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
     vconv[tid - 2 * DK] = y;
   }
   // ---- gates ----------------------------------------------------------------
-  const float beta = rbf(qh_sigmoid(bf2f(p.b[h])));
-  const float g = -__expf(p.A_log[h]) * qh_softplus(bf2f(p.a[h]) + p.dt_bias[h]);
+  const float beta = rbf(qh_sigmoid(bh));
+  const float g = -__expf(A_log) * qh_softplus(ah + dt_bias);
   const float decay = __expf(g);
   __syncthreads();
 
@@ -188,8 +199,8 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
   __syncthreads();
   if (rg == 0) {
     const float rs = rsqrtf((red2[0] + red2[1]) / (float)DV + p.eps);
-    const float normed = rbf(rbf(core * rs) * nw);
-    const float sz = rbf(qh_silu(zv));
+    const float normed = rbf(rbf(core * rs) * bf2f(nwraw));
+    const float sz = rbf(qh_silu(bf2f(zraw)));
     p.out[(size_t)h * DV + j] = f2bf(normed * sz);
   }
 }
