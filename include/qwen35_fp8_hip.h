@@ -78,12 +78,23 @@ void launch_fused_attn_v2(const void* q, const void* k_cache, const void* v_cach
                           int seq_len, int max_seq_len, int head_dim, int n_heads, int n_kv_heads,
                           qh_stream_t stream);
 
-/* replaces layer_pre_attn, fused_kernels.cu:1066-1091 (main.py:184-193) */
+/* replaces layer_pre_attn, fused_kernels.cu:1066-1091 (main.py:184-193).
+ * The checkpoint's q_proj rows are per-head [q_h | gate_h] (main.py:1001); the
+ * reference's opt-in fused path splits q_out as [first half | second half]
+ * (main.py:1292-1294).  With a q/gate head dim set (qh_set_qgate_head_dim, or
+ * the environment variable QH_QGATE_HEAD_DIM when it is left at -1), q_out is
+ * written de-interleaved, [q_0 .. q_{H-1} | gate_0 .. gate_{H-1}], which makes
+ * that split correct; with 0 (the default) the rows keep the checkpoint order. */
 void layer_pre_attn(const void* hidden, const float* norm_weight, const void* w_q, const void* s_q,
                     int N_q, int N_q_blk, const void* w_k, const void* s_k, int N_k, int N_k_blk,
                     const void* w_v, const void* s_v, int N_v, int N_v_blk, void* q_out,
                     void* k_out, void* v_out, void* norm_ws, int h_dim, int K_blk,
                     qh_stream_t stream);
+
+/* Head dim of layer_pre_attn's q/gate de-interleave: d > 0 on, 0 off, -1 (the
+ * initial value) follow QH_QGATE_HEAD_DIM.  No counterpart in the reference,
+ * whose opt-in path carries the split bug.  Returns 0, or -1 for d < -1. */
+int qh_set_qgate_head_dim(int d);
 
 /* replaces layer_post_attn, fused_kernels.cu:1102-1150 (main.py:194-206) */
 void layer_post_attn(const void* hidden, const void* attn_out, const void* w_o, const void* s_o,

@@ -54,6 +54,7 @@ NATIVE_SIGNATURES = {
     "qh_last_error": (ctypes.c_char_p, []),
     "qh_clear_error": (None, []),
     "qh_abi_version": (_i, []),
+    "qh_set_qgate_head_dim": (_i, [_i]),
     "qh_gemv_e4m3": (_i, [_vp, _vp, _vp, _f, _i, _vp, _vp, _i]
                      + [_vp, _vp, _vp, _i, _i] * 4 + [_i, _vp]),
     "qh_mlp_gate_up": (_i, [_vp, _vp, _vp, _f, _i, _vp, _vp, _vp, _vp, _i, _i,

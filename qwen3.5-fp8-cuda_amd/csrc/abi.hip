@@ -14,6 +14,7 @@
 // keeps one internal, grow-on-demand activation buffer (gemm.hip).
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "qh_attn.h"
@@ -52,6 +53,7 @@ QhGemvSeg seg(const void* w, const void* s, void* y, int n, int kb) {
   g.y = (uint16_t*)y;
   g.n = n;
   g.kb = kb;
+  g.qgate_d = 0;
   return g;
 }
 
@@ -207,6 +209,29 @@ QH_EXPORT void launch_fused_attn_v2(const void* q, const void* k_cache, const vo
             n_heads, n_kv_heads, stream);
 }
 
+// Q/gate layout of layer_pre_attn's q output.  The checkpoint's q_proj rows
+// are per-head [q_h | gate_h] (main.py:1001), but the reference's opt-in fused
+// full-attention path reads q_buf as [all q heads | all gates]
+// (main.py:1292-1294).  With a head dim d set here (or by the environment
+// variable QH_QGATE_HEAD_DIM, for an unmodified main.py), layer_pre_attn
+// stores q de-interleaved so that split is the right one; 0 keeps the
+// checkpoint order, like the reference kernel.
+static int g_qgate_d = -1;  // -1: take QH_QGATE_HEAD_DIM
+static int qgate_head_dim() {
+  if (g_qgate_d >= 0) return g_qgate_d;
+  const char* e = getenv("QH_QGATE_HEAD_DIM");
+  return e ? atoi(e) : 0;
+}
+
+QH_EXPORT int qh_set_qgate_head_dim(int d) {
+  if (d < -1) {
+    qh_set_error("qh_set_qgate_head_dim: d=%d (use -1, 0 or a head dim)", d);
+    return -1;
+  }
+  g_qgate_d = d;
+  return 0;
+}
+
 QH_EXPORT void layer_pre_attn(const void* hidden, const float* norm_weight, const void* w_q,
                               const void* s_q, int N_q, int N_q_blk, const void* w_k,
                               const void* s_k, int N_k, int N_k_blk, const void* w_v,
@@ -214,9 +239,20 @@ QH_EXPORT void layer_pre_attn(const void* hidden, const float* norm_weight, cons
                               void* v_out, void* norm_ws, int h_dim, int K_blk,
                               hipStream_t stream) {
   (void)N_q_blk; (void)N_k_blk; (void)N_v_blk;
+  const int d = qgate_head_dim();
+  if (d > 0 && (N_q % (2 * d)) != 0) {
+    qh_set_error("layer_pre_attn: N_q=%d is not a whole number of [q | gate] heads of 2 x %d", N_q,
+                 d);
+    return;
+  }
   qh_launch_rmsnorm_rows(hidden, norm_weight, norm_ws, 1, h_dim, 1e-6f, stream);
-  launch_fused_qkv(norm_ws, w_q, w_k, w_v, s_q, s_k, s_v, q_out, k_out, v_out, h_dim, N_q, N_k,
-                   N_v, K_blk, 0, 0, 0, stream);
+  QhGemvParams p = gemv_params(norm_ws, h_dim);
+  p.nseg = 3;
+  p.seg[0] = seg(w_q, s_q, q_out, N_q, K_blk);
+  p.seg[0].qgate_d = d > 0 ? d : 0;
+  p.seg[1] = seg(w_k, s_k, k_out, N_k, K_blk);
+  p.seg[2] = seg(w_v, s_v, v_out, N_v, K_blk);
+  run_gemv(p, true, "layer_pre_attn", stream);
 }
 
 QH_EXPORT void layer_post_o_fp8_mlp(const void* hidden, const void* o_out,

@@ -63,6 +63,16 @@ __host__ __device__ __forceinline__ uint32_t scale_count(int kb, int n) {
 }
 
 
+// Output index of segment row `row`: the identity, or for a gated q
+// projection (qgate_d = d, rows = H per-head blocks [q_h | gate_h] of 2d) the
+// de-interleaved position in [q_0 .. q_{H-1} | gate_0 .. gate_{H-1}].
+__device__ __forceinline__ int out_index(const QhGemvSeg& sg, int row) {
+  const int d = sg.qgate_d;
+  if (d <= 0) return row;
+  const int h = row / (2 * d), w = row - h * 2 * d;
+  return w < d ? h * d + w : (sg.n >> 1) + h * d + (w - d);
+}
+
 // ---- coherent activation I/O ----------------------------------------------------
 // Inside one launch of the chained kernel (below), activations pass between
 // workgroups that may sit on different XCDs, whose L2 caches are not coherent
@@ -457,7 +467,7 @@ __attribute__((amdgpu_waves_per_eu(gemv_min_waves(CPL)))) void gemv_e4m3_kernel(
           if (row < sg.n) {
             float y = rbf(acc[r]);
             if (p.res1) y = res[s][r] + y;
-            sg.y[row] = f2bf(y);
+            sg.y[out_index(sg, row)] = f2bf(y);
           }
         }
       }
@@ -720,7 +730,7 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
       if (lane == 0) {
         float y = rbf(acc);
         if (p.res1) y = res[s] + y;
-        st_act1<OUTC>(p.seg[sseg[s]].y + srow[s], f2bf(y));
+        st_act1<OUTC>(p.seg[sseg[s]].y + out_index(p.seg[sseg[s]], srow[s]), f2bf(y));
       }
       issue_w(w[s], sc[s], srow[s], sseg[s], g + P * stride);
       issue_res(res[s], srow[s], g + P * stride);

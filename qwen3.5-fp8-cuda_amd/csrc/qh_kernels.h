@@ -13,6 +13,8 @@ struct QhGemvSeg {
   uint16_t* y;       // bf16 [n]
   int n;             // rows
   int kb;            // scale-mode code (reference `K_blocks` encoding)
+  int qgate_d;       // 0: y[row]; d > 0: rows are per-head [q_h | gate_h] blocks
+                     // of 2d, stored de-interleaved as [q_0..q_{H-1} | gate_0..]
 };
 
 // Grouped GEMV sharing one activation vector.  Optional prologue: x := bf16(x +
