@@ -205,6 +205,29 @@ int qh_lm_head_argmax(const void* x, const float* norm_w, float eps, int K, cons
                       int64_t* tok_hist, int hist_len, int* pos_dev, const void* embed,
                       void* embed_out, qh_stream_t stream);
 
+/* Workspace bytes for qh_sample_top_p over a V-entry vocabulary. */
+size_t qh_sample_workspace_size(int V);
+
+/* replaces top_p_sample, main.py:49-87 (called at main.py:1726-1727): nucleus
+ * sampling of one bf16 logits row entirely on the device.  temperature > 0
+ * scales the logits; rep_penalty > 1 penalises the distinct ids of the window
+ * hist[max(lo, p - window) .. p), p = *pos_dev + pos_offset (pos when pos_dev
+ * is null), lo = *lo_dev (0 when null), window <= 64; top-min(2000, V)
+ * candidates normalised against the full vocabulary, full-softmax fallback
+ * when their mass is below top_p, top-p cut, one draw (SplitMix64 of seed and
+ * *counter, which advances by one).  Writes *tok_out, hist[p] when hist is
+ * given, and the token's row of embed [V, D] into h when embed is given.
+ * info (optional, 16 int64): cut key, kept at that key, kept count, fallback
+ * flag, kept mass (2^-40 units), draw bits, drawn key, rank, top-k mass, max,
+ * Z, log-partition (fp32 bits), token, counter used, window size.
+ * ws: qh_sample_workspace_size(V) bytes, 256-byte aligned, zeroed once (its
+ * arrival counters reset themselves); calls sharing one workspace must not
+ * overlap. */
+int qh_sample_top_p(const void* logits, int V, float temperature, float top_p, float rep_penalty,
+                    int64_t* hist, const int* pos_dev, int pos, int pos_offset, const int* lo_dev,
+                    int window, uint64_t seed, uint64_t* counter, void* ws, int64_t* tok_out,
+                    const void* embed, void* h, int D, int64_t* info, qh_stream_t stream);
+
 /* Embedding row gather (F.embedding, main.py:1587); ids outside [0, vocab)
  * give a zero row. */
 int qh_embed(const void* table, const int64_t* ids, void* out, int n, int K, int vocab,

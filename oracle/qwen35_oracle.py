@@ -17,7 +17,9 @@ explicit block-dequant path:
   * the batch prefill path (``_prefill_step`` main.py:1550-1566) with the
     fp32 torch attention of main.py:1034-1056 and the gated delta rule in its
     recurrent form (equal to transformers' chunked form up to fp32 rounding;
-    tests pin that against transformers' own function).
+    tests pin that against transformers' own function);
+  * top_p_sample (main.py:49-87) without the draw: the kept nucleus and its
+    probabilities.
 Nothing here imports the product package.
 """
 import math
@@ -320,6 +322,57 @@ def lm_head_argmax(h, norm_f, lm_head, eps=1e-6):
     xn = rmsnorm(h, norm_f, eps)
     logits = linear(xn, lm_head.float())
     return logits, argmax_first(logits)
+
+
+# ------------------------------------------------- sampling (main.py:49-87)
+def _recip32(x):
+    """fp32 reciprocal of a Python float: the reference divides a CUDA tensor by
+    a Python scalar, which PyTorch's CUDA kernel computes as a multiplication by
+    the fp32 reciprocal."""
+    return (torch.tensor(1.0, dtype=torch.float32) / torch.tensor(x, dtype=torch.float32)).item()
+
+
+def sample_scale(logits, temperature, rep_penalty=1.0, recent_ids=None):
+    """main.py:54-63 on a bf16 [V] row: y = bf16(x * (1/T)) when T > 0; then,
+    for each distinct recent id, bf16(y * rp) if y < 0 else bf16(y * (1/rp)).
+    Returns fp32 values of the bf16 tensor."""
+    y = logits.float().reshape(-1).clone()
+    if temperature > 0:
+        y = bf16(y * _recip32(temperature))
+    if rep_penalty > 1.0 and recent_ids:
+        ids = torch.tensor(sorted({int(i) for i in recent_ids}), dtype=torch.long)
+        r = y[ids]
+        y[ids] = torch.where(r < 0, bf16(r * rep_penalty), bf16(r * _recip32(rep_penalty)))
+    return y
+
+
+def sample_nucleus(logits, temperature=0.7, top_p=0.9, rep_penalty=1.0, recent_ids=None,
+                   topk=2000, logz_b=None, soft_mz=None):
+    """The kept prefix of top_p_sample (main.py:64-82), before the draw.
+
+    Tokens sorted by y descending, ties by index (a stable sort);
+    p = bf16(exp(bf16(y - bf16(logsumexp(y))))); when the top-min(topk, V)
+    mass, rounded to bf16, is below bf16(top_p), the full-vocabulary softmax
+    bf16(exp(y - max) / Z) instead; keep the prefix whose running mass, rounded
+    to bf16, stays <= bf16(top_p), at least one token.  logz_b and soft_mz =
+    (max, Z) override the log-partition and the softmax normaliser (to check a
+    cut with the device's fp32 sums).  Returns (ids, probs, fallback)."""
+    y = sample_scale(logits, temperature, rep_penalty, recent_ids)
+    V = y.numel()
+    order = torch.sort(y, descending=True, stable=True).indices
+    ys = y[order]
+    if logz_b is None:
+        logz_b = bf16(torch.logsumexp(y, 0)).item()
+    tp = bf16(torch.tensor(float(top_p))).item()
+    p = bf16(torch.exp(bf16(ys - logz_b)))
+    k = min(topk, V)
+    fallback = bf16(p[:k].double().sum().float()).item() < tp
+    if fallback:
+        M, Z = soft_mz if soft_mz is not None else (y.max().item(), torch.exp(y - y.max()).sum().item())
+        p = bf16(torch.exp(ys - M) / Z)
+    cum = bf16(torch.cumsum(p.double(), 0).float())
+    n = max(1, int((cum <= tp).sum()))  # cum is non-decreasing: the kept set is a prefix
+    return order[:n], p[:n], fallback
 
 
 # ------------------------------------------------------------------ model

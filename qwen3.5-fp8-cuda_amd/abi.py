@@ -22,6 +22,7 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _f = ctypes.c_float
 _sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
 
 # Reference ABI (fused_kernels.cu:940-1356, fp8_kernels.cu:68-91); argtypes as
 # declared by main.py:108-240.
@@ -70,6 +71,9 @@ NATIVE_SIGNATURES = {
     "qh_lm_head_scratch_bytes": (_sz, [_i]),
     "qh_lm_head_argmax": (_i, [_vp, _vp, _f, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i,
                                _vp, _vp, _vp, _vp]),
+    "qh_sample_workspace_size": (_sz, [_i]),
+    "qh_sample_top_p": (_i, [_vp, _i, _f, _f, _f, _vp, _vp, _i, _i, _vp, _i, _u64, _vp, _vp, _vp,
+                             _vp, _vp, _i, _vp, _vp]),
     "qh_embed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "qh_add_bf16": (_i, [_vp, _vp, _vp, _i, _vp]),
     "qh_linear_gates": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),

@@ -21,6 +21,7 @@
 #include "qh_gdn.h"
 #include "qh_gemm.h"
 #include "qh_prefill.h"
+#include "qh_sample.h"
 #include "qh_kernels.h"
 #include "qh_norm.h"
 
@@ -598,6 +599,39 @@ QH_EXPORT int qh_lm_head_argmax(const void* x, const float* norm_w, float eps, i
   p.embed_out = (uint16_t*)embed_out;
   if (qh_launch_lm_head(p, grid, stream) != 0) return -1;
   return check_launch("qh_lm_head_argmax");
+}
+
+QH_EXPORT size_t qh_sample_workspace_size(int V) { return qh_sample_workspace_bytes(V); }
+
+// Nucleus sampling of one bf16 logits row (main.py:49-87) on the device.
+QH_EXPORT int qh_sample_top_p(const void* logits, int V, float temperature, float top_p,
+                              float rep_penalty, int64_t* hist, const int* pos_dev, int pos,
+                              int pos_offset, const int* lo_dev, int window, uint64_t seed,
+                              uint64_t* counter, void* ws, int64_t* tok_out, const void* embed,
+                              void* h, int D, int64_t* info, hipStream_t stream) {
+  QhSampleParams p;
+  memset(&p, 0, sizeof(p));
+  p.logits = (const uint16_t*)logits;
+  p.V = V;
+  p.temperature = temperature;
+  p.top_p = top_p;
+  p.rep_penalty = rep_penalty;
+  p.hist = hist;
+  p.pos_dev = pos_dev;
+  p.pos = pos;
+  p.pos_offset = pos_offset;
+  p.lo_dev = lo_dev;
+  p.window = window;
+  p.seed = seed;
+  p.counter = counter;
+  p.ws = (uint8_t*)ws;
+  p.tok_out = tok_out;
+  p.embed = (const uint16_t*)embed;
+  p.h = (uint16_t*)h;
+  p.D = D;
+  p.info = info;
+  if (qh_launch_sample(p, stream) != 0) return -1;
+  return check_launch("qh_sample_top_p");
 }
 
 QH_EXPORT int qh_embed(const void* table, const int64_t* ids, void* out, int n, int K, int vocab,

@@ -81,6 +81,13 @@ class Qwen35FP8Engine:
         self.lm_scratch = torch.zeros(int(self.lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8,
                                       device=dev)
         self.lm_counter = torch.zeros(1, dtype=torch.int32, device=dev)
+        # nucleus sampling (off: greedy argmax, the benchmark path)
+        self.sampling = None
+        self.sample_ws = torch.zeros(int(self.lib.qh_sample_workspace_size(V)), dtype=torch.uint8,
+                                     device=dev)
+        self.sample_ctr = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.gen_lo = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.sample_info = torch.zeros(16, dtype=torch.int64, device=dev)
         self.attn_splits = attn_splits or default_attn_splits(max_seq_len)
         nbytes = int(self.lib.qh_attn_scratch_bytes(cfg.num_key_value_heads, self.attn_splits,
                                                     cfg.head_dim))
@@ -120,8 +127,9 @@ class Qwen35FP8Engine:
 
     # ------------------------------------------------------------------ state
     def _reset_cache(self):
-        """Zero GatedDeltaNet conv/recurrent states; position 0 (main.py:851-895).
-        KV-cache contents need no clearing: every readable slot is rewritten."""
+        """Zero GatedDeltaNet conv/recurrent states; position 0 (main.py:851-895);
+        the sampler's draw counter back to 0.  KV-cache contents need no
+        clearing: every readable slot is rewritten."""
         for r in self.conv_ring:
             if r is not None:
                 r.zero_()
@@ -129,6 +137,7 @@ class Qwen35FP8Engine:
             if s is not None:
                 s.zero_()
         self.pos.zero_()
+        self.sample_ctr.zero_()
 
     # ------------------------------------------------------------- launches
     def _gemv(self, x, segs, norm_w=None, res=None):
@@ -245,6 +254,34 @@ class Qwen35FP8Engine:
             abi.ptr(self.w.embed) if next_embed else None,
             abi.ptr(self.h) if next_embed else None, abi.stream_handle()), "lm_head_argmax")
 
+    def set_sampling(self, temperature=None, top_p=0.9, rep_penalty=1.0, window=50, seed=0):
+        """Sample instead of taking the argmax, with the reference's top_p_sample
+        semantics (main.py:49-87; temperature / top-p / repetition penalty over
+        the last `window` generated tokens, main.py:1720-1731).  temperature=None
+        restores greedy decoding.  A captured graph is dropped: capture again."""
+        if temperature is None:
+            self.sampling = None
+        else:
+            if not 0 <= window <= 64:
+                raise ValueError("window must be in [0, 64]")
+            self.sampling = dict(temperature=float(temperature), top_p=float(top_p),
+                                 rep_penalty=float(rep_penalty), window=int(window), seed=int(seed))
+        self.graph = None
+
+    def _sample(self):
+        """Replace the argmax the head just wrote (token, history slot pos - 1,
+        next embedding) by a draw from the nucleus of the same logits."""
+        sp = self.sampling
+        if sp is None:
+            return
+        cfg = self.cfg
+        abi.check(self.lib.qh_sample_top_p(
+            abi.ptr(self.logits), cfg.vocab_size, sp["temperature"], sp["top_p"], sp["rep_penalty"],
+            abi.ptr(self.tok_hist), abi.ptr(self.pos), 0, -1, abi.ptr(self.gen_lo), sp["window"],
+            sp["seed"], abi.ptr(self.sample_ctr), abi.ptr(self.sample_ws), abi.ptr(self.tok),
+            abi.ptr(self.w.embed), abi.ptr(self.h), cfg.hidden_size, abi.ptr(self.sample_info),
+            abi.stream_handle()), "sample_top_p")
+
     def _pre(self, i):
         self._gemv(self.h, self._in_segs(i), norm_w=self.w.layers[i]["input_layernorm"])
 
@@ -266,6 +303,7 @@ class Qwen35FP8Engine:
                 if i + 1 < n:
                     self._pre(i + 1)
         self._head()
+        self._sample()
 
     # ------------------------------------------------------------ graphs
     def capture(self):
@@ -304,6 +342,8 @@ class Qwen35FP8Engine:
                              f"max_seq_len={self.max_seq_len}")
         if logits_to_keep != 1:
             raise ValueError("only logits_to_keep=1 is supported")
+        # the sampler's repetition window starts at the first generated token
+        self.gen_lo.fill_(past_len + s - 1)
         if s > 1 and past_len == 0 and self.batch_prefill:
             return self.prefill_batch(ids)
         st = abi.stream_handle()
@@ -431,14 +471,16 @@ class Qwen35FP8Engine:
             cfg.vocab_size, abi.ptr(self.logits), abi.ptr(self.lm_scratch),
             abi.ptr(self.lm_counter), abi.ptr(self.tok), abi.ptr(self.tok_hist), self.max_seq_len,
             abi.ptr(self.pos), abi.ptr(self.w.embed), abi.ptr(self.h), st), "lm_head_argmax")
+        self._sample()
         return self.logits.view(1, -1)
 
     def generate(self, n_steps):
-        """n greedy steps from the current device state (no host sync)."""
+        """n decode steps (greedy, or sampled after set_sampling) from the
+        current device state (no host sync)."""
         for _ in range(n_steps):
             self.step()
 
     def tokens(self, start, stop):
-        """Greedy tokens chosen at positions [start, stop) (device tensor):
+        """Tokens chosen at positions [start, stop) (device tensor):
         tokens(t, t+1) is the token predicted after consuming position t."""
         return self.tok_hist[start:stop]
