@@ -51,7 +51,7 @@ def mlp_bytes(cfg):
 
 
 # The gate/up kernel the decode step launches (name as rocprofv3 reports it).
-GATE_UP_KERNEL = "mlp_fast_kernel<5, 1, float>(QhMlpParams)"
+GATE_UP_KERNEL = "mlp_fast_kernel<5, 1, float, 256>(QhMlpParams)"
 
 
 def measured_traffic():
