@@ -127,6 +127,68 @@ def traffic_probe(eng, reps=2, copy_mib=256):
                       "copies": 4}))
 
 
+FP8_MFMA_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 matrix-core peak
+
+
+def prefill_gemm_inputs(seed=0):
+    """BASELINE configs[2] (prefill FP8 GEMM): a CPU generator seeded `seed`
+    draws X [512, 2560], W [9216, 2560] * 0.02, X' [512, 9216], W' [2560, 9216]
+    * 0.02 in that order; W, W' quantized to E4M3 with fp32 128x128 scale_inv;
+    copied to the GPU."""
+    from qwen35_amd import synth
+    g = torch.Generator().manual_seed(seed)
+    x1 = torch.randn(512, 2560, generator=g).to(torch.bfloat16)
+    w1 = synth.quantize_block_fp8(torch.randn(9216, 2560, generator=g) * 0.02)
+    x2 = torch.randn(512, 9216, generator=g).to(torch.bfloat16)
+    w2 = synth.quantize_block_fp8(torch.randn(2560, 9216, generator=g) * 0.02)
+    cu = lambda t: t.to("cuda")
+    return [(cu(x1), cu(w1[0]), cu(w1[1])), (cu(x2), cu(w2[0]), cu(w2[1]))]
+
+
+def prefill_gemm_launchers(inputs):
+    """One launcher per config-3a GEMM (qh_gemm_e4m3: activation split +
+    matrix-core GEMM, on the current stream)."""
+    from qwen35_amd import abi
+    lib = abi.load()
+    out = []
+    for x, w, s in inputs:
+        M, K = x.shape
+        N = w.shape[0]
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device="cuda")
+
+        def run(x=x, w=w, s=s, y=y, ws=ws, M=M, N=N, K=K):
+            abi.check(lib.qh_gemm_e4m3(abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M, N, K,
+                                       K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm")
+        out.append(((M, N, K), run))
+    return out
+
+
+def time_prefill_gemm(reps=20):
+    """Config-3a GEMMs timed with HIP events on their stream (mean of `reps`
+    launches after warm-up); TFLOP/s = 2*M*N*K / time."""
+    res = []
+    for (M, N, K), run in prefill_gemm_launchers(prefill_gemm_inputs()):
+        for _ in range(3):
+            run()
+        st = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(reps):
+            run()
+        b.record(st)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        res.append({"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
+                    "frac_fp8_dense_peak": round(tf / FP8_MFMA_PEAK_TFLOPS, 4)})
+    return {"config": "BASELINE configs[2]: X[512x2560] x W[9216x2560]^T and X'[512x9216] x "
+                      "W'[2560x9216]^T, E4M3 128x128 block scales, seed 0",
+            "kernel": "quant_rows_kernel + gemm_e4m3_lds_kernel (v_mfma_scale_f32_32x32x64_f8f6f4; "
+                      "activation as hi+lo E4M3 terms: two fp8 products per multiply-add)",
+            "peak_tflops": FP8_MFMA_PEAK_TFLOPS, "gemms": res}
+
+
 def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
     """CPU oracle decode on the host cores.  Returns (tok/s over the timed
     greedy steps, threads, setup seconds, prompt, oracle tokens, oracle logits
@@ -191,6 +253,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--prefill-gemm-probe", action="store_true",
+                    help="only run the config-3a prefill GEMMs (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU (batch-1 decode runs on a single MI355X; "
@@ -202,6 +266,14 @@ def main():
 
     __graft_entry__.load_package()
     from qwen35_amd import config, engine, synth
+
+    if args.prefill_gemm_probe:
+        for _, run in prefill_gemm_launchers(prefill_gemm_inputs()):
+            for _ in range(4):
+                run()
+        torch.cuda.synchronize()
+        print(json.dumps({"prefill_gemm_probe": True, "launches_per_gemm": 4}))
+        return
 
     cfg = config.qwen35_4b()
     w = synth.make_weights(cfg, seed=args.seed, device="cuda")
@@ -234,6 +306,9 @@ def main():
     traffic, tk = measured_traffic()
     traffic_src = (f"profiles/gate_up_traffic_pmc.json ({tk})" if traffic is not None else None)
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
+    gemm = time_prefill_gemm()
+    log("prefill GEMM: " + ", ".join(f"{g['N']}x{g['K']} {g['us']} us ({g['tflops']} TFLOP/s)"
+                                     for g in gemm["gemms"]))
 
     # short greedy parity sample (GPU engine vs CPU oracle, same weights)
     cpu = None
@@ -293,6 +368,7 @@ def main():
             "launches_timed": n_launch,
         },
         "cpu_baseline": cpu,
+        "prefill_gemm": gemm,
         "parity": parity,
     }
     print(json.dumps(out))
