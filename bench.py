@@ -255,6 +255,9 @@ def main():
                     help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--prefill-gemm-probe", action="store_true",
                     help="only run the config-3a prefill GEMMs (for rocprofv3 --pmc)")
+    ap.add_argument("--decode-probe", action="store_true",
+                    help="only run 3 eager decode steps after a short prompt, then a calibration "
+                         "copy (for rocprofv3 --pmc per decode kernel)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU (batch-1 decode runs on a single MI355X; "
@@ -283,6 +286,20 @@ def main():
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
     if args.traffic_probe:
         traffic_probe(eng)
+        return
+    if args.decode_probe:
+        # context ~300 like the timed steps: a 300-token prompt, then eager steps
+        eng.prefill(synth.make_prompt(cfg, n=300, seed=args.seed + 1, device="cuda").view(1, -1))
+        for _ in range(3):
+            eng.step()
+        torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"decode_probe": True, "eager_steps": 3, "context": 300,
+                          "copy_bytes": 256 << 20, "copies": 4}))
         return
     eng.capture()
     log("decode step captured")
