@@ -17,8 +17,8 @@
 // there are enough tiles), a 2 x 2 grid of waves each holding (BM/2) x (BN/2)
 // of 32x32 matrix-core tiles.  Each 128-wide K block of A hi, A lo and B is
 // staged once per workgroup in LDS (rows padded to 144 bytes against bank
-// conflicts, two stages), the next block in registers while the current one
-// is multiplied.  Within a K block, lane half h of a 32x32x64 instruction
+// conflicts, one or two stages), the next one or two blocks in registers
+// while the current one is multiplied.  Within a K block, lane half h of a 32x32x64 instruction
 // takes bytes [64q + 32h, +32) of its row in both operands: the same K
 // permutation on A and B leaves the contraction unchanged.
 #include <mutex>
@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* x, uint
 }
 
 // gfx950 variant: operands staged through LDS once per workgroup (the four
-// waves of a 128x128 tile share its A and B rows), the next K block loaded
-// into registers while the current one is multiplied, and the 32x32x64 fp8
+// waves of a tile share its A and B rows), the next K blocks loaded into
+// registers while the current one is multiplied, and the 32x32x64 fp8
 // matrix-core instruction (its block-scale operands fixed at 2^0: the
 // checkpoint's fp32 block scale is applied per 128-wide K block in fp32).
 // A, A_lo and B rows of a K block are 128 bytes; LDS rows are padded to 144
@@ -92,7 +92,11 @@ __device__ __forceinline__ v8i lds_v8(const uint8_t* p) {
 // LDS bytes of one K-block stage of a BM x BN tile: A hi, A lo (BM rows), B (BN rows).
 constexpr int gemm_stage_bytes(int bm, int bn) { return (2 * bm + bn) * kGRow; }
 
-template <typename ScaleT, int BM, int BN>
+// NST LDS stages (1 or 2) and D K blocks in flight in registers.  The K loop
+// is unrolled by D so the register sets rotate statically; loads past the
+// last block re-read it (no branch, so the in-order load counter waits only
+// for the block about to be stored).  Requires (K / 128) % D == 0.
+template <typename ScaleT, int BM, int BN, int NST, int D>
 __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, const uint8_t* xlo,
                                                             const float* sx, const uint8_t* w,
                                                             const ScaleT* sw, uint16_t* y, int M,
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   constexpr int STAGE = gemm_stage_bytes(BM, BN);
   constexpr int PIECES = (2 * BM + BN) * 8;      // 16-byte pieces per K block
   constexpr int PPT = PIECES / 256;              // per thread
-  static_assert(PIECES % 256 == 0 && TI >= 1 && TJ >= 1, "tile shape");
+  static_assert(PIECES % 256 == 0 && TI >= 1 && TJ >= 1 && (NST == 1 || NST == 2), "tile shape");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -110,30 +114,31 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
   const int wm = (wid >> 1) * WM, wn = (wid & 1) * WN;
   const int r = lane & 31, h = lane >> 5;
+  const int KB = K / 128;
 
   // Global -> register staging: piece p is (operand row, 16-byte column) of
   // the stage's rows [A hi (BM) | A lo (BM) | B (BN)].
-  u32x4 st[PPT];
-  auto gload = [&](int kb) {
-    const int ko = kb * 128;
+  u32x4 st[D][PPT];
+  auto gload = [&](u32x4 (&dst)[PPT], int kb) {
+    const int ko = min(kb, KB - 1) * 128;
 #pragma unroll
     for (int e = 0; e < PPT; ++e) {
       const int piece = tid + 256 * e;
       const int row = piece >> 3, c16 = (piece & 7) * 16;
       if (row < 2 * BM) {
         const int m = min(mb + (row % BM), M - 1);
-        st[e] = *(const u32x4*)((row < BM ? xhi : xlo) + (size_t)m * K + ko + c16);
+        dst[e] = *(const u32x4*)((row < BM ? xhi : xlo) + (size_t)m * K + ko + c16);
       } else {
         const int n = min(nb + row - 2 * BM, N - 1);
-        st[e] = __builtin_nontemporal_load((const u32x4*)(w + (size_t)n * K + ko + c16));
+        dst[e] = __builtin_nontemporal_load((const u32x4*)(w + (size_t)n * K + ko + c16));
       }
     }
   };
-  auto sstore = [&](uint8_t* stage) {
+  auto sstore = [&](uint8_t* stage, const u32x4 (&src)[PPT]) {
 #pragma unroll
     for (int e = 0; e < PPT; ++e) {
       const int piece = tid + 256 * e;
-      *(u32x4*)(stage + (piece >> 3) * kGRow + (piece & 7) * 16) = st[e];
+      *(u32x4*)(stage + (piece >> 3) * kGRow + (piece & 7) * 16) = src[e];
     }
   };
 
@@ -145,13 +150,7 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int KB = K / 128;
-  gload(0);
-  sstore(smem);
-  __syncthreads();
-  for (int kb = 0; kb < KB; ++kb) {
-    const uint8_t* cur = smem + (kb & 1) * STAGE;
-    if (kb + 1 < KB) gload(kb + 1);
+  auto mma_block = [&](const uint8_t* cur, int kb) {
     float swj[TJ];
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -191,8 +190,27 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(t[i][j][e], swj[j], acc[i][j][e]);
-    if (kb + 1 < KB) sstore(smem + ((kb + 1) & 1) * STAGE);
-    __syncthreads();
+  };
+
+  // Prologue: blocks 0..D-1 in registers, block 0 in LDS stage 0, block D
+  // loaded into the freed register set.
+#pragma unroll
+  for (int d = 0; d < D; ++d) gload(st[d], d);
+  sstore(smem, st[0]);
+  gload(st[0], D);
+  __syncthreads();
+  // Invariant at step k: LDS stage (k % NST) holds block k, register set
+  // (k + 1) % D holds block k + 1.
+  for (int k0 = 0; k0 < KB; k0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int k = k0 + d;
+      mma_block(smem + (NST == 2 ? (k & 1) * STAGE : 0), k);
+      if constexpr (NST == 1) __syncthreads();   // one stage: every wave is done reading it
+      sstore(smem + (NST == 2 ? ((k + 1) & 1) * STAGE : 0), st[(d + 1) % D]);
+      gload(st[(d + 1) % D], k + 1 + D);
+      __syncthreads();
+    }
   }
 
   // C layout of a 32x32 tile: lane -> column lane%32, value e -> row
@@ -213,13 +231,27 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   }
 }
 
-template <typename ScaleT, int BM, int BN>
+template <typename ScaleT, int BM, int BN, int NST, int D>
 void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const void* w,
                      const void* s, void* y, int M, int N, int K, int kb, hipStream_t st) {
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BM, BN>), grid, dim3(256),
-                     2 * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx, (const uint8_t*)w,
-                     (const ScaleT*)s, (uint16_t*)y, M, N, K, kb);
+  hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BM, BN, NST, D>), grid, dim3(256),
+                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx,
+                     (const uint8_t*)w, (const ScaleT*)s, (uint16_t*)y, M, N, K, kb);
+}
+
+// 64x64 tiles.  With at least three tiles per CU, one LDS stage (27.6 KB)
+// lets four workgroups share a CU; with fewer tiles, two stages and two K
+// blocks in flight per workgroup.  M = 512: 9216 x 2560 50 us (1 stage) vs
+// 55 us (2 stages); 2560 x 9216 67 us (2 stages, 2 in flight) vs 70 us.
+template <typename ScaleT>
+void launch_gemm_small(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const void* w,
+                       const void* s, void* y, int M, int N, int K, int kb, hipStream_t st,
+                       int cus) {
+  const long tiles = (long)((N + 63) / 64) * ((M + 63) / 64);
+  if (tiles >= 3L * cus) launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+  else if ((K / 128) % 2 == 0) launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+  else launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
 }
 
 std::mutex g_ws_mu;
@@ -250,11 +282,11 @@ int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y,
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   const bool small = (long)((N + 127) / 128) * ((M + 127) / 128) < 2L * cus;
   if (small) {
-    if (scale_bf16) launch_gemm_lds<uint16_t, 64, 64>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
-    else launch_gemm_lds<float, 64, 64>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, w, s, y, M, N, K, kb, st, cus);
+    else launch_gemm_small<float>(xhi, xlo, sx, w, s, y, M, N, K, kb, st, cus);
   } else {
-    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
-    else launch_gemm_lds<float, 128, 128>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+    else launch_gemm_lds<float, 128, 128, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
   }
   return 0;
 }

@@ -476,7 +476,11 @@ def test_argmax_nan_logits_stay_in_bounds():
 
 
 # ------------------------------------------------------------------ prefill GEMM
-@pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256)])
+# (512, 9216, 2560): 64x64 tiles, one LDS stage; (512, 2560, 9216): two stages,
+# two K blocks in flight; (5, 256, 384): odd K-block count; (700, 9000, 2560):
+# ragged one-stage tiles; (2000, 4100, 384): ragged 128x128 tiles.
+@pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256),
+                                   (700, 9000, 2560), (2000, 4100, 384)])
 def test_gemm_e4m3(M, N, K):
     """BASELINE config 3a: X bf16 [M, K] . deq(W)^T through the fp8 matrix cores."""
     g = gen(M + N + K)
