@@ -164,6 +164,23 @@ def prefill_gemm_launchers(inputs):
     return out
 
 
+def time_prefill(eng, prompt, reps=3):
+    """Batch prefill of `prompt` (every projection as an FP8 GEMM, batch
+    attention / GatedDeltaNet kernels, lm_head + argmax of the last token):
+    best wall time of `reps` runs from the first launch to the token on the
+    device (host launch overhead included), as prompt-to-first-token."""
+    best = float("inf")
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.prefill(prompt.view(1, -1))
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    n = prompt.numel()
+    return {"prompt_tokens": n, "ms": round(best * 1e3, 3), "tok_per_s": round(n / best, 1),
+            "timing": f"wall clock, best of {reps}, synchronized before and after"}
+
+
 def time_prefill_gemm(reps=20):
     """Config-3a GEMMs timed with HIP events on their stream (mean of `reps`
     launches after warm-up); TFLOP/s = 2*M*N*K / time."""
@@ -253,6 +270,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run the batch prefill of the bench prompt 3 times (for rocprofv3)")
     ap.add_argument("--prefill-gemm-probe", action="store_true",
                     help="only run the config-3a prefill GEMMs (for rocprofv3 --pmc)")
     ap.add_argument("--decode-probe", action="store_true",
@@ -286,6 +305,10 @@ def main():
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
     if args.traffic_probe:
         traffic_probe(eng)
+        return
+    if args.prefill_probe:
+        prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
+        print(json.dumps({"prefill_probe": True, **time_prefill(eng, prompt)}))
         return
     if args.decode_probe:
         # context ~300 like the timed steps: a 300-token prompt, then eager steps
@@ -323,6 +346,8 @@ def main():
     traffic, tk = measured_traffic()
     traffic_src = (f"profiles/gate_up_traffic_pmc.json ({tk})" if traffic is not None else None)
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
+    prefill = time_prefill(eng, prompt)
+    log(f"prefill: {prefill['prompt_tokens']} tokens in {prefill['ms']} ms")
     gemm = time_prefill_gemm()
     log("prefill GEMM: " + ", ".join(f"{g['N']}x{g['K']} {g['us']} us ({g['tflops']} TFLOP/s)"
                                      for g in gemm["gemms"]))
@@ -385,6 +410,7 @@ def main():
             "launches_timed": n_launch,
         },
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "prefill_gemm": gemm,
         "parity": parity,
     }

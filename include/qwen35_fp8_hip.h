@@ -252,6 +252,17 @@ size_t qh_gemm_workspace_size(int M, int K);
 int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
                  int kb, int scales_bf16, void* ws, qh_stream_t stream);
 
+/* Grouped prefill GEMM; no counterpart in the reference, which runs each
+ * projection as its own fp8_gemm_batch (main.py:262-269).  Up to 4 projections
+ * of one activation x [M, K] (segment t: y_t [M, n_t] = bf16(x . deq(w_t)^T),
+ * scale mode kb_t), one activation split and one launch; ws as for
+ * qh_gemm_e4m3 (qh_gemm_workspace_size(M, K) bytes, required). */
+int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0, const void* s0,
+                         void* y0, int n0, int kb0, const void* w1, const void* s1, void* y1,
+                         int n1, int kb1, const void* w2, const void* s2, void* y2, int n2,
+                         int kb2, const void* w3, const void* s3, void* y3, int n3, int kb3,
+                         int scales_bf16, void* ws, qh_stream_t stream);
+
 /* One phase of a chained launch.  kind 1: grouped E4M3 GEMV (segments
  * w/s/y/n/kb as in qh_gemv_e4m3, optional (1+w) RMSNorm prologue and
  * residual res1 [+ res2]); kind 2: gate/up MLP (w[0]/s[0] gate, w[1]/s[1] up,

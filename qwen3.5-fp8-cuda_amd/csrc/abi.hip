@@ -678,6 +678,29 @@ QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y,
   return check_launch("qh_gemm_e4m3");
 }
 
+// Grouped prefill GEMM (no reference counterpart: the reference runs each
+// projection as its own fp8_gemm_batch, main.py:262-269).  Up to 4
+// projections of the same activation X[M, K] -- segment t:
+// Y_t[M, n_t] = bf16(X . deq(W_t)^T), scale mode kb_t -- with one activation
+// split and one launch.  `ws` as for qh_gemm_e4m3.
+QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0,
+                                   const void* s0, void* y0, int n0, int kb0, const void* w1,
+                                   const void* s1, void* y1, int n1, int kb1, const void* w2,
+                                   const void* s2, void* y2, int n2, int kb2, const void* w3,
+                                   const void* s3, void* y3, int n3, int kb3, int scales_bf16,
+                                   void* ws, hipStream_t stream) {
+  if (!k_ok(K, "qh_gemm_e4m3_grouped")) return -1;
+  if (!x || !ws) {
+    qh_set_error("qh_gemm_e4m3_grouped: null activation or workspace");
+    return -1;
+  }
+  if (M <= 0) return 0;
+  const QhGemmSeg seg[4] = {{w0, s0, y0, n0, kb0}, {w1, s1, y1, n1, kb1},
+                            {w2, s2, y2, n2, kb2}, {w3, s3, y3, n3, kb3}};
+  if (qh_launch_gemm_e4m3_group_ws(x, M, K, seg, nseg, scales_bf16 != 0, ws, stream) != 0) return -1;
+  return check_launch("qh_gemm_e4m3_grouped");
+}
+
 // Chained decode phases (no reference counterpart: the reference launches each
 // projection separately, fused_kernels.cu:1156-1195 being its largest fusion).
 // Up to 4 dependent GEMV / gate-up phases in one launch; `sync` holds

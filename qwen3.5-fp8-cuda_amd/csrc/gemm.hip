@@ -89,18 +89,30 @@ __device__ __forceinline__ v8i lds_v8(const uint8_t* p) {
   return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
-// LDS bytes of one K-block stage of a BM x BN tile: A hi, A lo (BM rows), B (BN rows).
-constexpr int gemm_stage_bytes(int bm, int bn) { return (2 * bm + bn) * kGRow; }
+// LDS bytes of one K-block stage of a BM x BN tile: A hi, A lo (BM rows), B
+// (BN rows), then the BN fp32 weight scales of the block.
+constexpr int gemm_stage_bytes(int bm, int bn) { return (2 * bm + bn) * kGRow + bn * 4; }
 
 // NST LDS stages (1 or 2) and D K blocks in flight in registers.  The K loop
 // is unrolled by D so the register sets rotate statically; loads past the
 // last block re-read it (no branch, so the in-order load counter waits only
 // for the block about to be stored).  Requires (K / 128) % D == 0.
+// Up to four projections of the same activation in one launch: segment t
+// owns N tiles [tstart[t], tstart[t + 1]) of the grid's x dimension.
+struct GemmGroup {
+  const uint8_t* w[4];
+  const void* s[4];
+  uint16_t* y[4];
+  int N[4];
+  int kb[4];
+  int tstart[4];
+  int nseg;
+};
+
 template <typename ScaleT, int BM, int BN, int NST, int D>
 __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, const uint8_t* xlo,
-                                                            const float* sx, const uint8_t* w,
-                                                            const ScaleT* sw, uint16_t* y, int M,
-                                                            int N, int K, int kb_code) {
+                                                            const float* sx, GemmGroup g, int M,
+                                                            int K) {
   constexpr int WM = BM / 2, WN = BN / 2;        // this wave's sub-tile (2 x 2 waves)
   constexpr int TI = WM / 32, TJ = WN / 32;      // 32x32 matrix-core tiles per wave
   constexpr int STAGE = gemm_stage_bytes(BM, BN);
@@ -111,16 +123,34 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = tid >> 6;
-  const int mb = blockIdx.y * BM, nb = blockIdx.x * BN;
+  // this workgroup's segment (uniform across the workgroup)
+  int si = 0;
+#pragma unroll
+  for (int t = 1; t < 4; ++t)
+    if (t < g.nseg && (int)blockIdx.x >= g.tstart[t]) si = t;
+  const uint8_t* w = g.w[si];
+  const ScaleT* sw = (const ScaleT*)g.s[si];
+  uint16_t* y = g.y[si];
+  const int N = g.N[si], kb_code = g.kb[si];
+  const int mb = blockIdx.y * BM, nb = ((int)blockIdx.x - g.tstart[si]) * BN;
   const int wm = (wid >> 1) * WM, wn = (wid & 1) * WN;
   const int r = lane & 31, h = lane >> 5;
   const int KB = K / 128;
 
   // Global -> register staging: piece p is (operand row, 16-byte column) of
   // the stage's rows [A hi (BM) | A lo (BM) | B (BN)].
+  // The block's weight scales travel with its operands and are staged in LDS
+  // beside them: a scale loaded at use time would sit behind every prefetched
+  // block in the in-order load counter and drain the pipeline at each K step.
+  // Thread t loads the scale of tile column t % BN (every thread loads, so no
+  // load sits under a branch).
+  constexpr int SC_OFF = (2 * BM + BN) * kGRow;
   u32x4 st[D][PPT];
-  auto gload = [&](u32x4 (&dst)[PPT], int kb) {
-    const int ko = min(kb, KB - 1) * 128;
+  float scv[D];
+  auto gload = [&](u32x4 (&dst)[PPT], float& sdst, int kb) {
+    kb = min(kb, KB - 1);
+    const int ko = kb * 128;
+    sdst = load_scale<ScaleT>(sw, scale_index(kb_code, min(nb + tid % BN, N - 1), kb));
 #pragma unroll
     for (int e = 0; e < PPT; ++e) {
       const int piece = tid + 256 * e;
@@ -134,12 +164,13 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
       }
     }
   };
-  auto sstore = [&](uint8_t* stage, const u32x4 (&src)[PPT]) {
+  auto sstore = [&](uint8_t* stage, const u32x4 (&src)[PPT], float sc) {
 #pragma unroll
     for (int e = 0; e < PPT; ++e) {
       const int piece = tid + 256 * e;
       *(u32x4*)(stage + (piece >> 3) * kGRow + (piece & 7) * 16) = src[e];
     }
+    if (tid < BN) *(float*)(stage + SC_OFF + tid * 4) = sc;
   };
 
   v16f acc[TI][TJ];
@@ -150,13 +181,10 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  auto mma_block = [&](const uint8_t* cur, int kb) {
+  auto mma_block = [&](const uint8_t* cur) {
     float swj[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int n = min(nb + wn + 32 * j + r, N - 1);
-      swj[j] = load_scale<ScaleT>(sw, scale_index(kb_code, n, kb));
-    }
+    for (int j = 0; j < TJ; ++j) swj[j] = *(const float*)(cur + SC_OFF + (wn + 32 * j + r) * 4);
     v16f t[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -195,9 +223,9 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   // Prologue: blocks 0..D-1 in registers, block 0 in LDS stage 0, block D
   // loaded into the freed register set.
 #pragma unroll
-  for (int d = 0; d < D; ++d) gload(st[d], d);
-  sstore(smem, st[0]);
-  gload(st[0], D);
+  for (int d = 0; d < D; ++d) gload(st[d], scv[d], d);
+  sstore(smem, st[0], scv[0]);
+  gload(st[0], scv[0], D);
   __syncthreads();
   // Invariant at step k: LDS stage (k % NST) holds block k, register set
   // (k + 1) % D holds block k + 1.
@@ -205,10 +233,11 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int k = k0 + d;
-      mma_block(smem + (NST == 2 ? (k & 1) * STAGE : 0), k);
+      mma_block(smem + (NST == 2 ? (k & 1) * STAGE : 0));
       if constexpr (NST == 1) __syncthreads();   // one stage: every wave is done reading it
-      sstore(smem + (NST == 2 ? ((k + 1) & 1) * STAGE : 0), st[(d + 1) % D]);
-      gload(st[(d + 1) % D], k + 1 + D);
+      const int nx = (d + 1) % D;   // static once the loop is unrolled
+      sstore(smem + (NST == 2 ? ((k + 1) & 1) * STAGE : 0), st[nx], scv[nx]);
+      gload(st[nx], scv[nx], k + 1 + D);
       __syncthreads();
     }
   }
@@ -231,13 +260,31 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   }
 }
 
+template <int BN>
+GemmGroup make_group(const QhGemmSeg* seg, int nseg, int& tiles_n) {
+  GemmGroup g = {};
+  g.nseg = nseg;
+  tiles_n = 0;
+  for (int t = 0; t < nseg; ++t) {
+    g.w[t] = (const uint8_t*)seg[t].w;
+    g.s[t] = seg[t].s;
+    g.y[t] = (uint16_t*)seg[t].y;
+    g.N[t] = seg[t].N;
+    g.kb[t] = seg[t].kb;
+    g.tstart[t] = tiles_n;
+    tiles_n += (seg[t].N + BN - 1) / BN;
+  }
+  return g;
+}
+
 template <typename ScaleT, int BM, int BN, int NST, int D>
-void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const void* w,
-                     const void* s, void* y, int M, int N, int K, int kb, hipStream_t st) {
-  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
+                     int nseg, int M, int K, hipStream_t st) {
+  int tiles_n = 0;
+  const GemmGroup g = make_group<BN>(seg, nseg, tiles_n);
+  dim3 grid(tiles_n, (M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BM, BN, NST, D>), grid, dim3(256),
-                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx,
-                     (const uint8_t*)w, (const ScaleT*)s, (uint16_t*)y, M, N, K, kb);
+                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx, g, M, K);
 }
 
 // 64x64 tiles.  With at least three tiles per CU, one LDS stage (27.6 KB)
@@ -245,13 +292,11 @@ void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, co
 // blocks in flight per workgroup.  M = 512: 9216 x 2560 50 us (1 stage) vs
 // 55 us (2 stages); 2560 x 9216 67 us (2 stages, 2 in flight) vs 70 us.
 template <typename ScaleT>
-void launch_gemm_small(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const void* w,
-                       const void* s, void* y, int M, int N, int K, int kb, hipStream_t st,
-                       int cus) {
-  const long tiles = (long)((N + 63) / 64) * ((M + 63) / 64);
-  if (tiles >= 3L * cus) launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
-  else if ((K / 128) % 2 == 0) launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
-  else launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+void launch_gemm_small(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
+                       int nseg, int M, int K, long tiles, hipStream_t st, int cus) {
+  if (tiles >= 3L * cus) launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
+  else if ((K / 128) % 2 == 0) launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, seg, nseg, M, K, st);
+  else launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
 }
 
 std::mutex g_ws_mu;
@@ -264,11 +309,24 @@ size_t qh_gemm_workspace_bytes(int M, int K) {
   return (size_t)M * K * 2 + (size_t)M * sizeof(float) + 256;
 }
 
-int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y, int M, int N,
-                           int K, int kb, bool scale_bf16, void* ws, hipStream_t st) {
+int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* seg, int nseg,
+                                 bool scale_bf16, void* ws, hipStream_t st) {
   if (K % 128 != 0) {
     qh_set_error("gemm: K=%d must be a multiple of 128", K);
     return -1;
+  }
+  if (nseg < 1 || nseg > 4) {
+    qh_set_error("gemm: nseg=%d outside [1, 4]", nseg);
+    return -1;
+  }
+  long tiles64 = 0, tiles128 = 0;
+  for (int t = 0; t < nseg; ++t) {
+    if (!seg[t].w || !seg[t].s || !seg[t].y || seg[t].N <= 0) {
+      qh_set_error("gemm: segment %d: null pointer or N=%d", t, seg[t].N);
+      return -1;
+    }
+    tiles64 += (seg[t].N + 63) / 64;
+    tiles128 += (seg[t].N + 127) / 128;
   }
   uint8_t* xhi = (uint8_t*)ws;
   uint8_t* xlo = xhi + (size_t)M * K;
@@ -280,15 +338,22 @@ int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y,
   // measured faster (M = 512: 63 vs 89 us for 9216 x 2560).
   int cus = 256, dev = 0;
   if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const bool small = (long)((N + 127) / 128) * ((M + 127) / 128) < 2L * cus;
+  const bool small = tiles128 * ((M + 127) / 128) < 2L * cus;
   if (small) {
-    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, w, s, y, M, N, K, kb, st, cus);
-    else launch_gemm_small<float>(xhi, xlo, sx, w, s, y, M, N, K, kb, st, cus);
+    const long tiles = tiles64 * ((M + 63) / 64);
+    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus);
+    else launch_gemm_small<float>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus);
   } else {
-    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
-    else launch_gemm_lds<float, 128, 128, 2, 1>(xhi, xlo, sx, w, s, y, M, N, K, kb, st);
+    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
+    else launch_gemm_lds<float, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
   }
   return 0;
+}
+
+int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y, int M, int N,
+                           int K, int kb, bool scale_bf16, void* ws, hipStream_t st) {
+  const QhGemmSeg seg = {w, s, y, N, kb};
+  return qh_launch_gemm_e4m3_group_ws(x, M, K, &seg, 1, scale_bf16, ws, st);
 }
 
 // Without a caller workspace, the library keeps one internal buffer that grows

@@ -397,6 +397,21 @@ class Qwen35FP8Engine:
                                         int(s.dtype == torch.bfloat16), abi.ptr(ws),
                                         abi.stream_handle()), "gemm")
 
+    def _gemm_group(self, x, segs, M, ws):
+        """Projections [((w, s), y), ...] of the same activation x in one
+        qh_gemm_e4m3_grouped launch (1 to 4 segments, one activation split)."""
+        args = []
+        for i in range(4):
+            if i < len(segs):
+                (w, s), y = segs[i]
+                args += [abi.ptr(w), abi.ptr(s), abi.ptr(y), w.shape[0], ops.scale_mode(w, s)]
+            else:
+                args += [None, None, None, 0, 0]
+        w0, s0 = segs[0][0]
+        abi.check(self.lib.qh_gemm_e4m3_grouped(abi.ptr(x), M, w0.shape[1], len(segs), *args,
+                                                int(s0.dtype == torch.bfloat16), abi.ptr(ws),
+                                                abi.stream_handle()), "gemm_grouped")
+
     def prefill_batch(self, ids):
         """The reference's s > 1 prefill (main.py:1550-1566) for a prompt at
         position 0: every projection as an FP8 GEMM over the M tokens, batch
@@ -423,9 +438,8 @@ class Qwen35FP8Engine:
             if cfg.is_full(i):
                 D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
                 q_all, k, v = B["q_all"][:M], B["k"][:M], B["v"][:M]
-                self._gemm(hn, ly["q_proj"], q_all, M, ws)
-                self._gemm(hn, ly["k_proj"], k, M, ws)
-                self._gemm(hn, ly["v_proj"], v, M, ws)
+                self._gemm_group(hn, [(ly["q_proj"], q_all), (ly["k_proj"], k),
+                                      (ly["v_proj"], v)], M, ws)
                 abi.check(L.qh_attn_prep(abi.ptr(q_all), abi.ptr(k), abi.ptr(v),
                                          abi.ptr(ly["q_norm"]), abi.ptr(ly["k_norm"]),
                                          abi.ptr(self.rope_cos), abi.ptr(self.rope_sin),
@@ -440,10 +454,9 @@ class Qwen35FP8Engine:
             else:
                 Hk, Hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
                 dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
-                self._gemm(hn, ly["in_proj_qkv"], B["mixed"][:M], M, ws)
-                self._gemm(hn, ly["in_proj_z"], B["z"][:M], M, ws)
-                self._gemm(hn, ly["in_proj_b"], B["b"][:M], M, ws)
-                self._gemm(hn, ly["in_proj_a"], B["a"][:M], M, ws)
+                self._gemm_group(hn, [(ly["in_proj_qkv"], B["mixed"][:M]), (ly["in_proj_z"], B["z"][:M]),
+                                      (ly["in_proj_b"], B["b"][:M]), (ly["in_proj_a"], B["a"][:M])],
+                                 M, ws)
                 abi.check(L.qh_gdn_prep(abi.ptr(B["mixed"]), abi.ptr(self.conv_ring[i]),
                                         abi.ptr(ly["conv1d_w"]), abi.ptr(B["a"]), abi.ptr(B["b"]),
                                         abi.ptr(ly["A_log"]), abi.ptr(ly["dt_bias"]),
@@ -459,8 +472,8 @@ class Qwen35FP8Engine:
             abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
             abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(ly["post_attention_layernorm"]),
                                    abi.ptr(hn), M, H, eps, st), "rmsnorm")
-            self._gemm(hn, ly["gate_proj"], B["gu_g"][:M], M, ws)
-            self._gemm(hn, ly["up_proj"], B["gu_u"][:M], M, ws)
+            self._gemm_group(hn, [(ly["gate_proj"], B["gu_g"][:M]), (ly["up_proj"], B["gu_u"][:M])],
+                             M, ws)
             abi.check(L.qh_silu_mul(abi.ptr(B["gu_g"]), abi.ptr(B["gu_u"]), abi.ptr(B["m"]), M * I,
                                     st), "silu_mul")
             self._gemm(B["m"][:M], ly["down_proj"], o, M, ws)

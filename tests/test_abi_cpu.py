@@ -86,6 +86,17 @@ def test_validation_errors_need_no_gpu():
     assert rc == -1 and "dk" in abi.last_error()
     rc = lib.qh_gemm_e4m3(None, None, None, None, 4, 4, 100, 1, 0, None, None)
     assert rc == -1
+    # grouped GEMM: every check runs before anything touches a device pointer
+    none4 = [None, None, None, 0, 0] * 4
+    rc = lib.qh_gemm_e4m3_grouped(None, 4, 2560, 1, *none4, 0, None, None)
+    assert rc == -1 and "null activation" in abi.last_error()
+    fake = ctypes.c_void_p(256)
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 5, *none4, 0, fake, None)
+    assert rc == -1 and "nseg=5" in abi.last_error()
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 1, *none4, 0, fake, None)
+    assert rc == -1 and "segment 0" in abi.last_error()
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 100, 1, *none4, 0, fake, None)
+    assert rc == -1
     # reference symbols: no error channel in the reference; ours records one
     lib.qh_clear_error()
     lib.launch_gemv_v4_extern(None, None, None, None, 16, 12, 1, None)

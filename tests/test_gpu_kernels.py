@@ -496,3 +496,30 @@ def test_gemm_e4m3(M, N, K):
     sync()
     ref16 = x.float() @ orc.dequant(w, s.to(torch.bfloat16).float()).t()
     assert cos_sim(y16.cpu().float(), ref16) >= 0.99999
+
+
+@pytest.mark.parametrize("M", [128, 37])
+def test_gemm_grouped_matches_single_launches(M):
+    """qh_gemm_e4m3_grouped (the prefill's in_proj shape: 8192 / 4096 / 32 / 32
+    rows of one activation) against one qh_gemm_e4m3 per segment, bit for bit
+    (each output tile runs the same K loop), and against the fp32 reference."""
+    g = gen(40 + M)
+    K, ns = 2560, (8192, 4096, 32, 32)
+    x = bf(randn(g, M, K))
+    ws_ = [quant(g, n, K) for n in ns]
+    lib = abi.load()
+    ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
+    dx = cu(x)
+    dw = [(cu(w), cu(s)) for w, s in ws_]
+    yg = [torch.empty(M, n, dtype=torch.bfloat16, device=DEV) for n in ns]
+    args = []
+    for (w, s), y, n in zip(dw, yg, ns):
+        args += [abi.ptr(w), abi.ptr(s), abi.ptr(y), n, ops.scale_mode(w, s)]
+    abi.check(lib.qh_gemm_e4m3_grouped(abi.ptr(dx), M, K, 4, *args, 0, abi.ptr(ws),
+                                       abi.stream_handle()), "grouped")
+    ys = [ops.fp8_linear(dx, w, s) for w, s in dw]
+    sync()
+    for a, b, (w, s), n in zip(yg, ys, ws_, ns):
+        assert torch.equal(a, b), f"grouped vs single launch differ for the {n}-row segment"
+        ref = x.float() @ orc.dequant(w, s).t()
+        assert cos_sim(a.cpu().float(), ref) >= 0.99999

@@ -67,9 +67,13 @@ def test_attention_prefill(M, past_fill):
     assert_close(out, ref, atol_frac=1e-3, what="prefill attention")
 
 
-def test_gdn_prefill():
-    g = gen(22)
-    M, Hk, Hv, dk, dv = 45, 2, 4, 128, 128
+# M = 45: five full 8-token blocks of the scan plus a tail; M = 3: fewer
+# tokens than the conv window (the ring supplies them all); past > 0 with a
+# filled ring and state: the conv reads positions before the prompt.
+@pytest.mark.parametrize("M,past", [(45, 0), (3, 0), (8, 6), (21, 6)])
+def test_gdn_prefill(M, past):
+    g = gen(22 + M + past)
+    Hk, Hv, dk, dv = 2, 4, 128, 128
     C = 2 * Hk * dk + Hv * dv
     mixed = bf(randn(g, M, C))
     a, b = bf(randn(g, M, Hv)), bf(randn(g, M, Hv))
@@ -79,8 +83,10 @@ def test_gdn_prefill():
     dt_bias = torch.ones(Hv)
     norm_w = bf(1 + randn(g, dv, std=0.02))
     lib = abi.load()
-    ring = torch.zeros(C, 4, dtype=torch.bfloat16, device=DEV)
-    state = torch.zeros(Hv, dk, dv, dtype=torch.float32, device=DEV)
+    ring0 = bf(randn(g, C, 4)) if past else torch.zeros(C, 4)
+    state0 = randn(g, Hv, dk, dv, std=0.1) if past else torch.zeros(Hv, dk, dv)
+    ring = cu(ring0).to(torch.bfloat16)
+    state = cu(state0).float()
     y = torch.empty(M, C, dtype=torch.bfloat16, device=DEV)
     qn = torch.empty(M, Hk * dk, dtype=torch.bfloat16, device=DEV)
     kn = torch.empty_like(qn)
@@ -92,20 +98,23 @@ def test_gdn_prefill():
     st = abi.stream_handle()
     abi.check(lib.qh_gdn_prep(abi.ptr(dm), abi.ptr(ring), abi.ptr(dw), abi.ptr(da), abi.ptr(db),
                               abi.ptr(dA), abi.ptr(ddt), abi.ptr(y), abi.ptr(qn), abi.ptr(kn),
-                              abi.ptr(gg), abi.ptr(beta), M, Hk, Hv, dk, dv, 0, st))
+                              abi.ptr(gg), abi.ptr(beta), M, Hk, Hv, dk, dv, past, st))
     abi.check(lib.qh_gdn_scan(abi.ptr(qn), abi.ptr(kn), abi.ptr(y), abi.ptr(gg), abi.ptr(beta),
                               abi.ptr(dz), abi.ptr(dnw), abi.ptr(state), abi.ptr(out), M, Hk, Hv,
                               dk, dv, 1e-6, st))
     torch.cuda.synchronize()
     # oracle: OracleModel._gdn_prefill after the projections
+    # window history: slot (past - 3 + i) % 4 of the ring holds position past - 3 + i
     cs = torch.zeros(C, 4)
+    for i in range(3):
+        cs[:, 1 + i] = ring0.float()[:, (past - 3 + i) % 4]
     xt = torch.cat([cs, mixed.float().t()], dim=1)
     conv = torch.stack([(conv_w.float() * xt[:, j + 1:j + 5]).sum(1) for j in range(M)], dim=0)
     yr = orc.bf16(F.silu(orc.bf16(conv)))
     assert_close(y, yr, atol_frac=1e-3, what="conv")
-    ring_ref = torch.zeros(C, 4)
+    ring_ref = ring0.float().clone()
     for mm in range(max(0, M - 4), M):
-        ring_ref[:, mm % 4] = mixed[mm].float()
+        ring_ref[:, (past + mm) % 4] = mixed[mm].float()
     assert torch.equal(ring.cpu().float(), ring_ref)
     yg = y.cpu().float()   # continue from the GPU conv output (isolates the later stages)
     kd, r = Hk * dk, Hv // Hk
@@ -119,7 +128,7 @@ def test_gdn_prefill():
     qh = qn.cpu().float().view(M, Hk, dk).repeat_interleave(r, dim=1)
     kh = kn.cpu().float().view(M, Hk, dk).repeat_interleave(r, dim=1)
     vh = yg[:, 2 * kd:].reshape(M, Hv, dv)
-    S = torch.zeros(Hv, dk, dv)
+    S = state0.clone()
     o = orc.gated_delta_rule_seq(qh * (1.0 / math.sqrt(dk)), kh, vh, gg.cpu(), beta.cpu().float(), S)
     gated = orc.gated_rmsnorm(orc.bf16(o), z.float().view(M, Hv, dv), norm_w, 1e-6, bf16_steps=True)
     assert_close(out.view(M, Hv, dv), gated, atol_frac=1e-3, what="gated output")
