@@ -245,6 +245,24 @@ int qh_linear_gates(const void* a, const void* b, const float* A_log, const floa
 int qh_gated_rmsnorm(const void* core, const void* z, const void* w, void* out, int heads,
                      int head_dim, float eps, int bf16_steps, qh_stream_t stream);
 
+/* GatedDeltaNet decode step up to the bf16 core [Hv*dv] (no gated norm): one
+ * wave per value head and 8 value columns, conv ring and state updated in
+ * place.  No counterpart in the reference, whose delta_rule_decode_kernel
+ * (fused_kernels.cu:623-684) is followed by the gated norm as its own step;
+ * pair it with qh_gemv_e4m3_gated.  dk = dv = 128, Hv % 8 == 0. */
+int qh_gdn_decode_core(const void* mixed, const void* a, const void* b, void* conv_ring,
+                       const void* conv_w, const float* A_log, const float* dt_bias, float* state,
+                       void* core, const int* pos_dev, int pos, int Hk, int Hv, int dk, int dv,
+                       qh_stream_t stream);
+
+/* Single-segment E4M3 GEMV whose activation is the per-head gated RMSNorm of
+ * core with gate z (main.py:1152-1158, head dim d = 128), optional residual
+ * res.  No counterpart in the reference, which normalises and then runs
+ * launch_gemv_v4_extern.  K % 512 == 0, 128x128 block scales. */
+int qh_gemv_e4m3_gated(const void* core, const void* z, const void* norm_w, int d, float eps, int K,
+                       const void* res, const void* w, const void* s, void* y, int n, int kb,
+                       int scales_bf16, qh_stream_t stream);
+
 /* Workspace bytes for qh_gemm_e4m3. */
 size_t qh_gemm_workspace_size(int M, int K);
 

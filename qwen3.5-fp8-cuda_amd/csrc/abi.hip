@@ -560,6 +560,62 @@ QH_EXPORT int qh_gdn_decode(const void* mixed, const void* a, const void* b, con
   return check_launch("qh_gdn_decode");
 }
 
+// GatedDeltaNet decode step up to the bf16 core (no reference counterpart:
+// the reference's delta_rule_decode_kernel, fused_kernels.cu:623-684, is
+// followed by the gated norm as its own step).  One wave per value head and 8
+// value columns; the gated RMSNorm is qh_gemv_e4m3_gated's prologue.
+QH_EXPORT int qh_gdn_decode_core(const void* mixed, const void* a, const void* b, void* conv_ring,
+                                 const void* conv_w, const float* A_log, const float* dt_bias,
+                                 float* state, void* core, const int* pos_dev, int pos, int Hk,
+                                 int Hv, int dk, int dv, hipStream_t stream) {
+  if (!mixed || !a || !b || !conv_ring || !conv_w || !A_log || !dt_bias || !state || !core) {
+    qh_set_error("qh_gdn_decode_core: null pointer argument");
+    return -1;
+  }
+  QhGdnParams g;
+  memset(&g, 0, sizeof(g));
+  g.mixed = (const uint16_t*)mixed;
+  g.a = (const uint16_t*)a;
+  g.b = (const uint16_t*)b;
+  g.conv_ring = (uint16_t*)conv_ring;
+  g.conv_w = (const uint16_t*)conv_w;
+  g.A_log = A_log;
+  g.dt_bias = dt_bias;
+  g.state = state;
+  g.out = (uint16_t*)core;
+  g.pos_dev = pos_dev;
+  g.pos = pos;
+  g.Hk = Hk;
+  g.Hv = Hv;
+  g.dk = dk;
+  g.dv = dv;
+  if (qh_launch_gdn_decode_core(g, stream) != 0) return -1;
+  return check_launch("qh_gdn_decode_core");
+}
+
+// Single-segment E4M3 GEMV whose activation is the GatedDeltaNet gated
+// RMSNorm of core with gate z (main.py:1152-1158: per head of d = 128,
+// bf16(bf16(bf16(core * rs) * w) * bf16(silu(z)))), optional residual res.
+// No reference counterpart (the reference normalises, then runs
+// launch_gemv_v4_extern).  Fast-path shapes: K % 512 == 0, 128x128 scales.
+QH_EXPORT int qh_gemv_e4m3_gated(const void* core, const void* z, const void* norm_w, int d,
+                                 float eps, int K, const void* res, const void* w, const void* s,
+                                 void* y, int n, int kb, int scales_bf16, hipStream_t stream) {
+  if (!core || !z || !norm_w) {
+    qh_set_error("qh_gemv_e4m3_gated: null core, gate or norm weight");
+    return -1;
+  }
+  QhGemvParams p = gemv_params(core, K);
+  p.x2 = (const uint16_t*)z;
+  p.gnorm_w = (const uint16_t*)norm_w;
+  p.gnorm_d = d;
+  p.eps = eps;
+  p.res1 = (const uint16_t*)res;
+  p.nseg = 1;
+  p.seg[0] = seg(w, s, y, n, kb);
+  return run_gemv(p, scales_bf16 != 0, "qh_gemv_e4m3_gated", stream);
+}
+
 QH_EXPORT size_t qh_lm_head_scratch_bytes(int N) {
   return (size_t)qh_lm_head_grid(N) * (sizeof(float) + sizeof(int));
 }

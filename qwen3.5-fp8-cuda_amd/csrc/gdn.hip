@@ -205,6 +205,114 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
   }
 }
 
+// ---- decode step split by value columns: one wave per (value head, 8 columns) --
+// Same semantics as gdn_decode_kernel up to the bf16 core output, which goes
+// to `out`; the gated RMSNorm (needs a whole head, here spread over 16 waves)
+// is the output projection's prologue (qh_gemv_e4m3_gated).  Lane l owns
+// value column 8 cg + (l >> 3) and state rows 16 (l & 7) .. +16, so a wave
+// reads and writes 4 KB of state and its sums over the key dimension are
+// 8-lane DPP butterflies: no workgroup barrier anywhere.  Each wave recomputes
+// the conv + l2norm of its key head's q and k (two channels of each per lane,
+// full-wave sums).  Block b runs head b % Hv, column group b / Hv: the 16
+// waves of a head share the state's 128-byte lines and sit on one XCD (blocks
+// are dealt to the XCDs round-robin and Hv is a multiple of 8).
+constexpr int GDN_COLS = 8;
+
+__global__ __launch_bounds__(64) void gdn_decode_cols_kernel(QhGdnParams p) {
+  constexpr int DK = 128, DV = 128, L = 64 / GDN_COLS, RPT = DK / L;  // 8 lanes x 16 rows per column
+  __shared__ __align__(16) float sq[DK];
+  __shared__ __align__(16) float sk[DK];
+  const int h = (int)blockIdx.x % p.Hv, cg = (int)blockIdx.x / p.Hv;
+  const int r = p.Hv / p.Hk, kh = h / r;
+  const int lane = threadIdx.x;
+  const int rg = lane & (L - 1);
+  const int j = cg * GDN_COLS + lane / L;
+  const int t = p.pos_dev ? *p.pos_dev : p.pos;
+
+  // Small operands first (vector-memory loads complete in issue order), then
+  // the state slice: the conv, norms and gates run while it arrives.
+  const int cq = kh * DK + 2 * lane;             // q channels cq, cq + 1
+  const int ck = p.Hk * DK + kh * DK + 2 * lane;  // k channels ck, ck + 1
+  const int cv = 2 * p.Hk * DK + h * DV + j;      // this lane's v channel
+  const uint32_t xq = *(const uint32_t*)(p.mixed + cq), xk = *(const uint32_t*)(p.mixed + ck);
+  const uint16_t xv = p.mixed[cv];
+  const u32x4 ringq = *(const u32x4*)(p.conv_ring + (size_t)cq * 4);  // 2 channels x 4 slots
+  const u32x4 ringk = *(const u32x4*)(p.conv_ring + (size_t)ck * 4);
+  const u32x2 ringv = *(const u32x2*)(p.conv_ring + (size_t)cv * 4);
+  const u32x4 wq = *(const u32x4*)(p.conv_w + (size_t)cq * 4);
+  const u32x4 wk = *(const u32x4*)(p.conv_w + (size_t)ck * 4);
+  const u32x2 wv = *(const u32x2*)(p.conv_w + (size_t)cv * 4);
+  const float bh = bf2f(p.b[h]), ah = bf2f(p.a[h]);
+  const float A_log = p.A_log[h], dt_bias = p.dt_bias[h];
+  float* col = p.state + (size_t)h * DK * DV + j;
+  float S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) S[i] = col[(size_t)(rg * RPT + i) * DV];
+
+  // causal conv (window of 4) + SiLU of one channel: ring = its 4 slots (slot
+  // s holds x at positions = s mod 4), w = its 4 taps, x = x_t
+  auto conv = [&](uint32_t r01, uint32_t r23, uint32_t w01, uint32_t w23, float x) {
+    auto slot = [&](int sidx) {
+      const uint32_t wv2 = (sidx & 2) ? r23 : r01;
+      return (sidx & 1) ? bf_hi(wv2) : bf_lo(wv2);
+    };
+    float acc = bf_hi(w23) * x;
+    acc = fmaf(bf_lo(w23), slot((t + 3) & 3), acc);
+    acc = fmaf(bf_hi(w01), slot((t + 2) & 3), acc);
+    acc = fmaf(bf_lo(w01), slot((t + 1) & 3), acc);
+    return rbf(qh_silu(rbf(acc)));
+  };
+  const float q0 = conv(ringq.x, ringq.y, wq.x, wq.y, bf_lo(xq));
+  const float q1 = conv(ringq.z, ringq.w, wq.z, wq.w, bf_hi(xq));
+  const float k0 = conv(ringk.x, ringk.y, wk.x, wk.y, bf_lo(xk));
+  const float k1 = conv(ringk.z, ringk.w, wk.z, wk.w, bf_hi(xk));
+  const float v = conv(ringv.x, ringv.y, wv.x, wv.y, bf2f(xv));
+  // The ring's slot t: q/k channels are shared by the r value heads of a key
+  // head (written by column group 0 of its first value head), v by its head.
+  if (cg == 0 && h % r == 0) {
+    p.conv_ring[(size_t)cq * 4 + (t & 3)] = (uint16_t)(xq & 0xFFFFu);
+    p.conv_ring[(size_t)(cq + 1) * 4 + (t & 3)] = (uint16_t)(xq >> 16);
+    p.conv_ring[(size_t)ck * 4 + (t & 3)] = (uint16_t)(xk & 0xFFFFu);
+    p.conv_ring[(size_t)(ck + 1) * 4 + (t & 3)] = (uint16_t)(xk >> 16);
+  }
+  if (rg == 0) p.conv_ring[(size_t)cv * 4 + (t & 3)] = xv;
+
+  // l2norm of q and k over the key head (full-wave sums)
+  const float nq = wave_total(fmaf(q0, q0, q1 * q1));
+  const float nk = wave_total(fmaf(k0, k0, k1 * k1));
+  const float iq = rsqrtf(nq + 1e-6f) * rsqrtf((float)DK), ik = rsqrtf(nk + 1e-6f);
+  *(qh_f32x2*)(sq + 2 * lane) = qh_f32x2{q0 * iq, q1 * iq};
+  *(qh_f32x2*)(sk + 2 * lane) = qh_f32x2{k0 * ik, k1 * ik};
+  const float beta = rbf(qh_sigmoid(bh));
+  const float decay = __expf(-__expf(A_log) * qh_softplus(ah + dt_bias));
+  __syncthreads();  // one wave: orders the LDS writes before the reads
+  float kr[RPT], qr[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; i += 4) {
+    *(f32x4*)(kr + i) = *(const f32x4*)(sk + rg * RPT + i);
+    *(f32x4*)(qr + i) = *(const f32x4*)(sq + rg * RPT + i);
+  }
+
+  // delta rule on column j
+  float pp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    S[i] *= decay;
+    pp[i & 3] = fmaf(S[i], kr[i], pp[i & 3]);
+  }
+  const float pred = column_sum<L>((pp[0] + pp[1]) + (pp[2] + pp[3]));
+  const float delta = (v - pred) * beta;
+  float op[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    S[i] = fmaf(kr[i], delta, S[i]);
+    col[(size_t)(rg * RPT + i) * DV] = S[i];
+    op[i & 3] = fmaf(S[i], qr[i], op[i & 3]);
+  }
+  const float o = column_sum<L>((op[0] + op[1]) + (op[2] + op[3]));
+  p.out[(size_t)h * DV + j] = f2bf(o);  // the 8 lanes of the column store the same value
+}
+
 // Reference ABI delta rule (fused_kernels.cu:623-684): q, k already expanded to
 // one row per value head, g fp32, beta bf16, state updated in place, bf16 out.
 template <int DK>
@@ -258,6 +366,16 @@ int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st) {
     return -1;
   }
   hipLaunchKernelGGL(gdn_decode_kernel<128>, dim3(p.Hv), dim3(GDN_THREADS), 0, st, p);
+  return 0;
+}
+
+int qh_launch_gdn_decode_core(const QhGdnParams& p, hipStream_t st) {
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0 || p.Hv % 8 != 0) {
+    qh_set_error("gdn_core: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk = dv = 128, Hv %% 8 == 0)",
+                 p.dk, p.dv, p.Hk, p.Hv);
+    return -1;
+  }
+  hipLaunchKernelGGL(gdn_decode_cols_kernel, dim3(p.Hv * (128 / GDN_COLS)), dim3(64), 0, st, p);
   return 0;
 }
 

@@ -148,9 +148,13 @@ struct XIn {
 template <int CPL>
 constexpr bool early_x() { return CPL <= 8; }
 
+// gw: optional bf16 weights [gd] of a per-head gated RMSNorm (x = the
+// GatedDeltaNet core, x2 = its gate z); a chunk's 8 weights are kept in w0 as
+// raw bits.
 template <int CPL, bool COH = false, int NT = 256>
 __device__ __forceinline__ void block_x_load(XIn<CPL, NT>& in, const uint16_t* x, const uint16_t* x2,
-                                             const float* norm_w, int K) {
+                                             const float* norm_w, int K, const uint16_t* gw = nullptr,
+                                             int gd = 0) {
   const int tid = threadIdx.x;
   const int nch = K / 8;
 #pragma unroll
@@ -159,28 +163,57 @@ __device__ __forceinline__ void block_x_load(XIn<CPL, NT>& in, const uint16_t* x
     const int cc = c < nch ? c : 0;
     in.v[i] = ld_act8<COH>(x, cc * 8);
     if (x2) in.v2[i] = ld_act8<COH>(x2, cc * 8);
-    if (norm_w) {
+    if (gw) {
+      in.w0[i] = __builtin_bit_cast(f32x4, *(const u32x4*)(gw + (cc * 8) % gd));
+    } else if (norm_w) {
       in.w0[i] = *(const f32x4*)(norm_w + cc * 8);
       in.w1[i] = *(const f32x4*)(norm_w + cc * 8 + 4);
     }
   }
 }
 
+// Gated RMSNorm of one element with the reference's bf16 intermediates
+// (main.py:1152-1158): bf16(bf16(c * rs) * w) * bf16(silu(z)), then bf16.
+__device__ __forceinline__ float gated1(float c, float z, float rs, float w) {
+  return rbf(rbf(c * rs) * w) * rbf(qh_silu(z));
+}
+__device__ __forceinline__ u32x4 gated_bf16x8(u32x4 c, u32x4 z, float rs, u32x4 w) {
+  u32x4 r;
+  r.x = pack_bf2(gated1(bf_lo(c.x), bf_lo(z.x), rs, bf_lo(w.x)), gated1(bf_hi(c.x), bf_hi(z.x), rs, bf_hi(w.x)));
+  r.y = pack_bf2(gated1(bf_lo(c.y), bf_lo(z.y), rs, bf_lo(w.y)), gated1(bf_hi(c.y), bf_hi(z.y), rs, bf_hi(w.y)));
+  r.z = pack_bf2(gated1(bf_lo(c.z), bf_lo(z.z), rs, bf_lo(w.z)), gated1(bf_hi(c.z), bf_hi(z.z), rs, bf_hi(w.z)));
+  r.w = pack_bf2(gated1(bf_lo(c.w), bf_lo(z.w), rs, bf_lo(w.w)), gated1(bf_hi(c.w), bf_hi(z.w), rs, bf_hi(w.w)));
+  return r;
+}
+
 // Builds the (normalised) activation in LDS; returns after the barrier.
+// gd > 0: the per-head gated RMSNorm (heads of gd = 128 elements: a head's 16
+// chunks sit in 16 consecutive threads, an aligned lane group) instead of the
+// x2 sum and the (1+w) RMSNorm.
 template <int CPL, int NT = 256>
 __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, float* red, bool has_x2,
-                                               bool has_norm, float eps, int K) {
+                                               bool has_norm, float eps, int K, int gd = 0) {
   constexpr int MAXC = XIn<CPL, NT>::MAXC;
   const int tid = threadIdx.x;
   const int nch = K / 8;
   const u32x4 zero = {0u, 0u, 0u, 0u};
   u32x4 v[MAXC];
+  if (gd > 0) {
 #pragma unroll
-  for (int i = 0; i < MAXC; ++i) {
-    v[i] = has_x2 ? add_bf16x8(in.v[i], in.v2[i]) : in.v[i];
-    v[i] = tid + NT * i < nch ? v[i] : zero;
+    for (int i = 0; i < MAXC; ++i) {
+      const bool in_k = tid + NT * i < nch;
+      const float ss = column_sum<16>(sumsq_bf16x8(in_k ? in.v[i] : zero, 0.0f));
+      const float rs = rsqrtf(ss / (float)gd + eps);
+      v[i] = in_k ? gated_bf16x8(in.v[i], in.v2[i], rs, __builtin_bit_cast(u32x4, in.w0[i])) : zero;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      v[i] = has_x2 ? add_bf16x8(in.v[i], in.v2[i]) : in.v[i];
+      v[i] = tid + NT * i < nch ? v[i] : zero;
+    }
   }
-  if (has_norm) {
+  if (gd == 0 && has_norm) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
@@ -705,7 +738,7 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
   (void)res;
 
   XIn<CPL, NT> xin;
-  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K);
+  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
 #pragma unroll
   for (int s = 0; s < P; ++s) {
     if (!CH && s == fast_lead(CPL)) x_arrived(xin);
@@ -719,7 +752,8 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
     for (int s = 0; s < P; ++s) issue_res(res[s], srow[s], g + s * stride);
   }
   u32x4 xr[CPL];
-  block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
+                          p.gnorm_w ? p.gnorm_d : 0);
   x_slice<CPL>(xr, sx);
 
   for (;;) {
@@ -1159,6 +1193,12 @@ int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st) {
   if (p.gtotal == 0) return 0;
   bool fast = p.K % 512 == 0;
   for (int i = 0; i < p.nseg; ++i) fast = fast && p.seg[i].kb == p.K / 128;
+  if (p.gnorm_w && (!fast || p.gnorm_d != 128 || !p.x2 || p.norm_w)) {
+    qh_set_error("gemv: the gated-norm prologue needs K %% 512 == 0, 128x128 block scales, head "
+                 "dim 128 (got %d) and a gate vector, and excludes the (1+w) norm",
+                 p.gnorm_d);
+    return -1;
+  }
   if (fast) {
 #define F(C) (scale_bf16 ? launch_gemv_fast_t<C, uint16_t>(p, st) : launch_gemv_fast_t<C, float>(p, st))
     QH_FAST_DISPATCH(p.K / 512, F)

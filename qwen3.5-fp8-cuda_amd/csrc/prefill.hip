@@ -249,17 +249,6 @@ __global__ __launch_bounds__(64) void gdn_norm_gates_kernel(QhGdnPrepParams p) {
 // to `out`; gdn_gated_norm_kernel then applies the gated RMSNorm in place.
 constexpr int SCAN_AHEAD = 8;
 
-// Sum over the L lanes of a column (L = 8 or 16 consecutive lanes), in every
-// one of them: DPP quad swaps, then half-row and row mirrors.
-template <int L>
-__device__ __forceinline__ float column_sum(float x) {
-  x += dpp_src<0xB1, 0xF>(x);   // quad_perm [1,0,3,2]
-  x += dpp_src<0x4E, 0xF>(x);   // quad_perm [2,3,0,1]
-  x += dpp_src<0x141, 0xF>(x);  // row_half_mirror
-  if constexpr (L == 16) x += dpp_src<0x140, 0xF>(x);  // row_mirror
-  return x;
-}
-
 template <int COLS>
 __global__ __launch_bounds__(64) void gdn_scan_kernel(QhGdnScanParams p) {
   constexpr int DK = 128, DV = 128, A = SCAN_AHEAD;

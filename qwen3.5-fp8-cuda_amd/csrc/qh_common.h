@@ -100,6 +100,17 @@ __device__ __forceinline__ float wave_total(float v) {
   v += dpp_src<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+// Sum over aligned groups of L consecutive lanes (L = 8 or 16), in every lane
+// of the group: DPP quad swaps, then half-row and row mirrors.
+template <int L>
+__device__ __forceinline__ float column_sum(float x) {
+  static_assert(L == 8 || L == 16, "group of 8 or 16 lanes");
+  x += dpp_src<0xB1, 0xF>(x);   // quad_perm [1,0,3,2]
+  x += dpp_src<0x4E, 0xF>(x);   // quad_perm [2,3,0,1]
+  x += dpp_src<0x141, 0xF>(x);  // row_half_mirror
+  if constexpr (L == 16) x += dpp_src<0x140, 0xF>(x);  // row_mirror
+  return x;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QH_WAVE));

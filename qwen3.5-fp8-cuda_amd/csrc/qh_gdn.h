@@ -25,6 +25,8 @@ struct QhGdnParams {
 };
 
 int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st);
+// bf16 core output to p.out, no gated norm (one wave per head and 8 columns)
+int qh_launch_gdn_decode_core(const QhGdnParams& p, hipStream_t st);
 int qh_launch_delta_rule(const void* q, const void* k, const void* v, const float* g,
                          const void* beta, float* state, void* out, int n_heads, int head_dim,
                          hipStream_t st);

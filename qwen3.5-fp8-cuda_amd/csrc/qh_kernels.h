@@ -32,6 +32,10 @@ struct QhGemvParams {
   int gtotal;      // filled by the launcher
   int gstart[5];   // filled by the launcher
   QhGemvSeg seg[4];
+  // Optional per-head gated RMSNorm prologue (fast path only): x is the
+  // GatedDeltaNet core, x2 its gate z, gnorm_w the bf16 norm weights [gnorm_d].
+  const uint16_t* gnorm_w;
+  int gnorm_d;
 };
 
 // Paired gate/up GEMV with the SiLU(gate)*up epilogue (fp32 accumulators).

@@ -50,7 +50,7 @@ def default_attn_splits(max_seq):
 
 class Qwen35FP8Engine:
     def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda",
-                 use_chain=False, batch_prefill=True):
+                 use_chain=False, batch_prefill=True, split_gdn=True):
         if not torch.cuda.is_available():
             raise RuntimeError("Qwen35FP8Engine needs a GPU (there is no CPU fallback)")
         self.lib = abi.load()
@@ -118,6 +118,13 @@ class Qwen35FP8Engine:
         # Chained launches (qh_chain): per layer, the mixer's output projection,
         # gate/up, down and the next layer's input projection run as one launch.
         self.use_chain = use_chain and self._chain_shapes_ok()
+        # GatedDeltaNet decode split in two launches' worth of work: the step up
+        # to the bf16 core (qh_gdn_decode_core, one wave per head and 8 value
+        # columns), then the gated RMSNorm as the output projection's prologue
+        # (qh_gemv_e4m3_gated).  Needs head dims 128, Hv % 8 == 0 and the fast
+        # GEMV shape for out_proj; the chained path keeps the fused step.
+        self.split_gdn = split_gdn and not self.use_chain and self._split_gdn_ok()
+        self.gdn_core = torch.zeros(cfg.value_dim, **bf)
         if self.use_chain:
             words = int(self.lib.qh_chain_sync_words())
             self.chain_sync = torch.zeros(cfg.num_hidden_layers, words, dtype=torch.int32,
@@ -203,6 +210,19 @@ class Qwen35FP8Engine:
                                            eps=self.eps))
         return (abi.ChainPhase * len(ph))(*ph)
 
+    def _split_gdn_ok(self):
+        cfg = self.cfg
+        if (cfg.linear_key_head_dim, cfg.linear_value_head_dim) != (128, 128) \
+                or cfg.linear_num_value_heads % 8 != 0 or cfg.value_dim % 512 != 0:
+            return False
+        for i in range(cfg.num_hidden_layers):
+            if cfg.is_full(i):
+                continue
+            w, s = self.w.layers[i]["out_proj"]
+            if ops.scale_mode(w, s) != w.shape[1] // 128:
+                return False
+        return True
+
     def chain_error(self):
         """True if a chained launch's bounded wait expired (results invalid)."""
         return self.use_chain and int(self.chain_err.item()) != 0
@@ -221,6 +241,13 @@ class Qwen35FP8Engine:
                 cfg.num_attention_heads, cfg.num_key_value_heads, abi.ptr(self.pos), 0,
                 self.attn_splits, abi.ptr(self.attn_scratch), abi.ptr(self.attn_counters),
                 abi.ptr(self.mix_out), self.eps, st), "attn_decode")
+        elif self.split_gdn:
+            abi.check(L.qh_gdn_decode_core(
+                abi.ptr(self.mixed), abi.ptr(self.a), abi.ptr(self.b), abi.ptr(self.conv_ring[i]),
+                abi.ptr(ly["conv1d_w"]), abi.ptr(ly["A_log"]), abi.ptr(ly["dt_bias"]),
+                abi.ptr(self.state[i]), abi.ptr(self.gdn_core), abi.ptr(self.pos), 0,
+                cfg.linear_num_key_heads, cfg.linear_num_value_heads, cfg.linear_key_head_dim,
+                cfg.linear_value_head_dim, st), "gdn_decode_core")
         else:
             abi.check(L.qh_gdn_decode(
                 abi.ptr(self.mixed), abi.ptr(self.a), abi.ptr(self.b), abi.ptr(self.z),
@@ -235,7 +262,15 @@ class Qwen35FP8Engine:
         cfg, L, ly = self.cfg, self.lib, self.w.layers[i]
         st = abi.stream_handle()
         x, wo = self._out_proj(i)
-        self._gemv(x, [(wo, self.h2)], res=self.h)
+        if self.split_gdn and not cfg.is_full(i):
+            w, s = wo
+            abi.check(L.qh_gemv_e4m3_gated(
+                abi.ptr(self.gdn_core), abi.ptr(self.z), abi.ptr(ly["norm_w"]),
+                cfg.linear_value_head_dim, self.eps, cfg.value_dim, abi.ptr(self.h), abi.ptr(w),
+                abi.ptr(s), abi.ptr(self.h2), w.shape[0], ops.scale_mode(w, s),
+                int(s.dtype == torch.bfloat16), st), "gemv_gated")
+        else:
+            self._gemv(x, [(wo, self.h2)], res=self.h)
         wg, sg = ly["gate_proj"]
         wu, su = ly["up_proj"]
         abi.check(L.qh_mlp_gate_up(abi.ptr(self.h2), None, abi.ptr(ly["post_attention_layernorm"]),

@@ -29,11 +29,15 @@ def _run(cfg, n_prompt, n_steps, graph):
     return w, prompt, toks, first_logits, eng
 
 
+# tiny(): 4 GatedDeltaNet value heads, the fused decode step; lv_heads=8: the
+# split step (qh_gdn_decode_core + the gated out_proj prologue, Hv % 8 == 0).
 @pytest.mark.parametrize("graph", [False, True])
-def test_tiny_model_greedy_tokens_match_oracle(graph):
-    cfg = tiny(num_layers=4)
+@pytest.mark.parametrize("lk,lv", [(2, 4), (4, 8)])
+def test_tiny_model_greedy_tokens_match_oracle(graph, lk, lv):
+    cfg = tiny(num_layers=4, lk_heads=lk, lv_heads=lv)
     n_prompt, n_steps = 6, 12
-    w, prompt, toks, first_logits, _ = _run(cfg, n_prompt, n_steps, graph)
+    w, prompt, toks, first_logits, eng = _run(cfg, n_prompt, n_steps, graph)
+    assert eng.split_gdn == (lv % 8 == 0)
     ref = orc.OracleModel(w, max_seq_len=128, prefill="sequential")
     rl = ref.forward(prompt.view(1, -1), 0).view(-1)
     assert cos_sim(first_logits, rl) > 0.9999
@@ -75,13 +79,14 @@ def _wide(num_layers=4, vocab=4096):
 @pytest.mark.parametrize("graph", [False, True])
 def test_chained_launches_equal_separate_launches(graph):
     """The chained engine (out_proj/gate-up/down/next in_proj per launch, opt-in)
-    gives bit-identical logits and tokens to the engine launching each kernel."""
+    gives bit-identical logits and tokens to the engine launching each kernel
+    (with the same fused GatedDeltaNet step: split_gdn=False)."""
     cfg = _wide()
     w = make_weights(cfg, seed=3, device="cuda")
     prompt = make_prompt(cfg, n=5, seed=4)
     out = []
     for chain in (True, False):
-        eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=64, use_chain=chain)
+        eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=64, use_chain=chain, split_gdn=False)
         assert eng.use_chain == chain
         if graph:
             eng.capture()

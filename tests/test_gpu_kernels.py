@@ -366,6 +366,54 @@ def test_gdn_decode(t):
     assert int(counters.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("t", [7, 4096])
+def test_gdn_decode_core_and_gated_out_proj(t):
+    """The split decode step: qh_gdn_decode_core (one wave per head and 8
+    columns, bf16 core, conv ring and state updated) against the oracle, then
+    qh_gemv_e4m3_gated (gated RMSNorm prologue + out_proj + residual) against
+    the oracle from the GPU's own core."""
+    g = gen(t + 5)
+    Hk, Hv, dk, dv, H = 16, 32, 128, 128, 2560
+    d = _gdn_inputs(g, Hk, Hv, dk, dv)
+    kd = Hk * dk
+    st = d["conv_state"].float().clone()
+    y = orc.conv_update(d["mixed"].float(), st, d["conv_w"].float())
+    q = y[:kd].view(Hk, dk).repeat_interleave(2, 0)
+    k = y[kd:2 * kd].view(Hk, dk).repeat_interleave(2, 0)
+    v = y[2 * kd:].view(Hv, dv)
+    gg, beta = orc.linear_gates(d["a"].float(), d["b"].float(), d["A_log"], d["dt_bias"])
+    S = d["S"].clone()
+    core = orc.delta_rule_step(q, k, v, gg, beta, S)
+    lib = abi.load()
+    ring = cu(bf(_ring_from_ordered(d["conv_state"].float(), t)))
+    Sg = cu(d["S"])
+    coreg = torch.empty(Hv * dv, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gdn_decode_core(abi.ptr(cu(d["mixed"])), abi.ptr(cu(d["a"])), abi.ptr(cu(d["b"])),
+                                     abi.ptr(ring), abi.ptr(cu(d["conv_w"])), abi.ptr(cu(d["A_log"])),
+                                     abi.ptr(cu(d["dt_bias"])), abi.ptr(Sg), abi.ptr(coreg), None, t,
+                                     Hk, Hv, dk, dv, abi.stream_handle()), "gdn_core")
+    sync()
+    assert_close(coreg, orc.bf16(core.reshape(-1)), atol_frac=1e-3, what="gdn core (bf16)")
+    c = cos_sim(Sg.cpu(), S)
+    assert c > 0.999999, f"state cosine {c}"
+    assert torch.allclose(Sg.cpu(), S, rtol=1e-4, atol=1e-5)
+    assert torch.equal(ring.cpu().float(), _ring_from_ordered(st, t + 1)), "conv ring update"
+    # out_proj with the gated RMSNorm prologue and the residual
+    wo, so = quant(g, H, Hv * dv)
+    h = bf(randn(g, H))
+    h2 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    dwo, dso = cu(wo), cu(so)
+    abi.check(lib.qh_gemv_e4m3_gated(abi.ptr(coreg), abi.ptr(cu(d["z"])), abi.ptr(cu(d["norm_w"])), dv,
+                                     1e-6, Hv * dv, abi.ptr(cu(h)), abi.ptr(dwo), abi.ptr(dso),
+                                     abi.ptr(h2), H, ops.scale_mode(dwo, dso), 0,
+                                     abi.stream_handle()), "gemv_gated")
+    sync()
+    gated = orc.gated_rmsnorm(coreg.cpu().float().view(Hv, dv), d["z"].float().view(Hv, dv),
+                              d["norm_w"].float())
+    ref = orc.bf16(h.float() + orc.linear(gated.reshape(-1), orc.dequant(wo, so)))
+    assert_close(h2, ref, atol_frac=1e-3, what="gated out_proj + residual")
+
+
 def test_delta_rule_and_gates_reference_abi():
     g = gen(31)
     H, hd = 32, 128
