@@ -110,9 +110,12 @@ struct GemmGroup {
 };
 
 template <typename ScaleT, int BM, int BN, int NST, int D>
+// Split-K (part != null): blockIdx.z takes K blocks [z KB/S, (z+1) KB/S) of
+// S = gridDim.z and stores its fp32 partial tile, unscaled, at
+// part[(z M + m) ldp + global column]; gemm_splitk_reduce_kernel finishes.
 __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, const uint8_t* xlo,
                                                             const float* sx, GemmGroup g, int M,
-                                                            int K) {
+                                                            int K, float* part, int ldp) {
   constexpr int WM = BM / 2, WN = BN / 2;        // this wave's sub-tile (2 x 2 waves)
   constexpr int TI = WM / 32, TJ = WN / 32;      // 32x32 matrix-core tiles per wave
   constexpr int STAGE = gemm_stage_bytes(BM, BN);
@@ -135,7 +138,8 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   const int mb = blockIdx.y * BM, nb = ((int)blockIdx.x - g.tstart[si]) * BN;
   const int wm = (wid >> 1) * WM, wn = (wid & 1) * WN;
   const int r = lane & 31, h = lane >> 5;
-  const int KB = K / 128;
+  const int KB = K / 128 / (int)gridDim.z;        // K blocks of this workgroup
+  const int kb0 = (int)blockIdx.z * KB;
 
   // Global -> register staging: piece p is (operand row, 16-byte column) of
   // the stage's rows [A hi (BM) | A lo (BM) | B (BN)].
@@ -148,7 +152,7 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   u32x4 st[D][PPT];
   float scv[D];
   auto gload = [&](u32x4 (&dst)[PPT], float& sdst, int kb) {
-    kb = min(kb, KB - 1);
+    kb = kb0 + min(kb, KB - 1);
     const int ko = kb * 128;
     sdst = load_scale<ScaleT>(sw, scale_index(kb_code, min(nb + tid % BN, N - 1), kb));
 #pragma unroll
@@ -244,6 +248,20 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
 
   // C layout of a 32x32 tile: lane -> column lane%32, value e -> row
   // 8*(e/4) + 4*(lane/32) + e%4.
+  if (part) {
+    float* pz = part + (size_t)blockIdx.z * M * ldp;
+    const int ng0 = (int)blockIdx.x * BN;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = mb + wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) pz[(size_t)m * ldp + ng0 + wn + 32 * j + r] = acc[i][j][e];
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
 #pragma unroll
@@ -258,6 +276,31 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
       }
     }
   }
+}
+
+// Split-K finish: y = bf16(sx[m] * sum_z part[z][m][column]), summed in z
+// order; columns past a segment's N (tile padding) are skipped.  Four
+// columns per thread (segments start at multiples of 64 columns).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
+                                                                 int ldp, const float* sx,
+                                                                 GemmGroup g, int bn) {
+  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= (size_t)M * ldp / 4) return;
+  const int m = (int)(q / (ldp / 4)), ng = (int)(q % (ldp / 4)) * 4;
+  const int tile = ng / bn;
+  int si = 0;
+#pragma unroll
+  for (int t = 1; t < 4; ++t)
+    if (t < g.nseg && tile >= g.tstart[t]) si = t;
+  const int n = ng - g.tstart[si] * bn, N = g.N[si];
+  if (n >= N) return;
+  f32x4 acc = *(const f32x4*)(part + (size_t)m * ldp + ng);
+  for (int z = 1; z < S; ++z) acc += *(const f32x4*)(part + ((size_t)z * M + m) * ldp + ng);
+  const float s = sx[m];
+  uint16_t* y = g.y[si] + (size_t)m * N + n;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (n + c < N) y[c] = f2bf(acc[c] * s);
 }
 
 template <int BN>
@@ -279,24 +322,38 @@ GemmGroup make_group(const QhGemmSeg* seg, int nseg, int& tiles_n) {
 
 template <typename ScaleT, int BM, int BN, int NST, int D>
 void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
-                     int nseg, int M, int K, hipStream_t st) {
+                     int nseg, int M, int K, hipStream_t st, int S = 1, float* part = nullptr) {
   int tiles_n = 0;
   const GemmGroup g = make_group<BN>(seg, nseg, tiles_n);
-  dim3 grid(tiles_n, (M + BM - 1) / BM);
+  dim3 grid(tiles_n, (M + BM - 1) / BM, S);
+  const int ldp = tiles_n * BN;
   hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BM, BN, NST, D>), grid, dim3(256),
-                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx, g, M, K);
+                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx, g, M, K,
+                     S > 1 ? part : nullptr, ldp);
+  if (S > 1) {
+    const size_t quads = (size_t)M * ldp / 4;
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256),
+                       0, st, (const float*)part, S, M, ldp, sx, g, BN);
+  }
 }
 
 // 64x64 tiles.  With at least three tiles per CU, one LDS stage (27.6 KB)
 // lets four workgroups share a CU; with fewer tiles, two stages and two K
 // blocks in flight per workgroup.  M = 512: 9216 x 2560 50 us (1 stage) vs
 // 55 us (2 stages); 2560 x 9216 67 us (2 stages, 2 in flight) vs 70 us.
+// S > 1: split-K over S slices of K (partials in `part`); the variant is
+// chosen by the workgroup count tiles * S and the per-slice K block count.
 template <typename ScaleT>
 void launch_gemm_small(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
-                       int nseg, int M, int K, long tiles, hipStream_t st, int cus) {
-  if (tiles >= 3L * cus) launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
-  else if ((K / 128) % 2 == 0) launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, seg, nseg, M, K, st);
-  else launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
+                       int nseg, int M, int K, long tiles, hipStream_t st, int cus, int S,
+                       float* part) {
+  const int kbl = K / 128 / S;
+  if (tiles * S >= 3L * cus)
+    launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
+  else if (kbl % 2 == 0)
+    launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
+  else
+    launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
 }
 
 std::mutex g_ws_mu;
@@ -305,8 +362,14 @@ size_t g_ws_bytes = 0;
 
 }  // namespace
 
+// Workspace: the activation's hi and lo E4M3 terms (M x K bytes each), the
+// row scales, then the split-K partials.  A split GEMM runs S * tiles <= 3 per
+// CU workgroups of 64x64 fp32 partials, so kSplitPartBytes covers up to 1024
+// of them (341 CUs).
+constexpr size_t kSplitPartBytes = (size_t)1024 * 64 * 64 * sizeof(float);
+
 size_t qh_gemm_workspace_bytes(int M, int K) {
-  return (size_t)M * K * 2 + (size_t)M * sizeof(float) + 256;
+  return (size_t)M * K * 2 + (size_t)M * sizeof(float) + 512 + kSplitPartBytes;
 }
 
 int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* seg, int nseg,
@@ -341,8 +404,23 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   const bool small = tiles128 * ((M + 127) / 128) < 2L * cus;
   if (small) {
     const long tiles = tiles64 * ((M + 63) / 64);
-    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus);
-    else launch_gemm_small<float>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus);
+    // Split-K when there are no more tiles than CUs: the largest S <= 8
+    // dividing the K blocks with >= 4 blocks per slice and S * tiles <= 3 per
+    // CU, so each workgroup walks fewer serial K steps.  The extra reduce
+    // launch costs more than it saves above that (M = 128: 9216 x 2560, 288
+    // tiles, 24.7 us unsplit vs 28.8 us in 2; 2560 x 9216, 80 tiles, 46.5 vs
+    // 28.7 us in 8).
+    const int KB = K / 128;
+    int S = 1;
+    for (int c = 8; c >= 2 && tiles <= cus; --c)
+      if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
+          (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes) {
+        S = c;
+        break;
+      }
+    float* part = (float*)(((uintptr_t)(sx + M) + 255) & ~(uintptr_t)255);
+    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus, S, part);
+    else launch_gemm_small<float>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus, S, part);
   } else {
     if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
     else launch_gemm_lds<float, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);

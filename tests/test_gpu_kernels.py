@@ -525,10 +525,13 @@ def test_argmax_nan_logits_stay_in_bounds():
 
 # ------------------------------------------------------------------ prefill GEMM
 # (512, 9216, 2560): 64x64 tiles, one LDS stage; (512, 2560, 9216): two stages,
-# two K blocks in flight; (5, 256, 384): odd K-block count; (700, 9000, 2560):
-# ragged one-stage tiles; (2000, 4100, 384): ragged 128x128 tiles.
+# two K blocks in flight; (5, 256, 384): odd K-block count;
+# (700, 9000, 2560): ragged one-stage tiles; (2000, 4100, 384): ragged 128x128
+# tiles; (128, 2560, 4096), (37, 1000, 9216), (128, 32, 2560): split-K in 8, 8
+# (ragged N, one M tile) and 5.
 @pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256),
-                                   (700, 9000, 2560), (2000, 4100, 384)])
+                                   (700, 9000, 2560), (2000, 4100, 384), (128, 2560, 4096),
+                                   (37, 1000, 9216), (128, 32, 2560)])
 def test_gemm_e4m3(M, N, K):
     """BASELINE config 3a: X bf16 [M, K] . deq(W)^T through the fp8 matrix cores."""
     g = gen(M + N + K)
@@ -549,8 +552,10 @@ def test_gemm_e4m3(M, N, K):
 @pytest.mark.parametrize("M", [128, 37])
 def test_gemm_grouped_matches_single_launches(M):
     """qh_gemm_e4m3_grouped (the prefill's in_proj shape: 8192 / 4096 / 32 / 32
-    rows of one activation) against one qh_gemm_e4m3 per segment, bit for bit
-    (each output tile runs the same K loop), and against the fp32 reference."""
+    rows of one activation) against one qh_gemm_e4m3 per segment and against
+    the fp32 reference.  The two calls may split K differently (the split
+    count follows the tile count), so they agree to one bf16 ulp, not bit for
+    bit."""
     g = gen(40 + M)
     K, ns = 2560, (8192, 4096, 32, 32)
     x = bf(randn(g, M, K))
@@ -568,6 +573,6 @@ def test_gemm_grouped_matches_single_launches(M):
     ys = [ops.fp8_linear(dx, w, s) for w, s in dw]
     sync()
     for a, b, (w, s), n in zip(yg, ys, ws_, ns):
-        assert torch.equal(a, b), f"grouped vs single launch differ for the {n}-row segment"
+        assert_close(a, b, rtol=2 ** -7, atol_frac=1e-6, what=f"grouped vs single, {n} rows")
         ref = x.float() @ orc.dequant(w, s).t()
         assert cos_sim(a.cpu().float(), ref) >= 0.99999
