@@ -174,3 +174,31 @@ def test_engine_batch_prefill_matches_oracle_reference_prefill():
         lg, _ = ref.decode_token(t, pos)
         lg = lg.view(-1)
         pos += 1
+
+
+def test_engine_batch_prefill_4b_widths_matches_oracle():
+    """Batch prefill at the 4B layer widths (hidden 2560, MLP 9216, 16x256
+    attention, 32x128 GatedDeltaNet; 4 layers, small vocabulary): the grouped
+    GEMMs, split-K (out_proj / o_proj / down at M = 40 have fewer tiles than
+    CUs), the wave-per-columns scan and the batch attention, against the
+    oracle's reference prefill."""
+    import dataclasses
+    from qwen35_amd.config import qwen35_4b
+    cfg = dataclasses.replace(qwen35_4b(), num_hidden_layers=4, vocab_size=4096, layer_types=None)
+    w = make_weights(cfg, seed=5)
+    prompt = make_prompt(cfg, n=40, seed=6)
+    eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=64)
+    logits = eng.forward(prompt.view(1, -1).cuda(), 0).float().cpu().view(-1)
+    ref = orc.OracleModel(w, max_seq_len=64, prefill="reference")
+    rl = ref.forward(prompt.view(1, -1), 0).view(-1)
+    # At these widths the oracle's two exact restatements of the prompt pass
+    # (the reference's chunked prefill and the token-by-token recurrence)
+    # already disagree at the 1e-4 level of logit cosine (0.99982 at 4 layers,
+    # measured): the GPU path must agree with the reference prefill as well as
+    # they agree with each other.
+    rs = orc.OracleModel(w, max_seq_len=64, prefill="sequential").forward(prompt.view(1, -1), 0).view(-1)
+    c, c_oracle = cos_sim(logits, rl), cos_sim(rs, rl)
+    assert c > 0.9995 and c >= c_oracle - 1e-4, f"logit cosine {c} (oracle paths: {c_oracle})"
+    top = torch.topk(rl, 2).values
+    if float(top[0] - top[1]) > 2 ** -6:
+        assert int(torch.argmax(logits)) == orc.argmax_first(rl)
