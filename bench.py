@@ -21,6 +21,10 @@ Also reported on the same JSON line:
                on a bounded sample of decode steps of the same model.
   parity       greedy tokens of the GPU engine vs the CPU oracle on a short
                prompt (the oracle is the checker here, never the product).
+  prefill      wall time of the batch prefill of the prompt.
+  prefill_gemm BASELINE configs[2] FP8 GEMMs on the matrix cores.
+  kernels      BASELINE configs 1, 2, 3b, 4a, 4b kernel by kernel over input
+               copies that exceed the MALL, with the CPU timings of each.
 """
 import argparse
 import json
@@ -206,6 +210,225 @@ def time_prefill_gemm(reps=20):
             "peak_tflops": FP8_MFMA_PEAK_TFLOPS, "gemms": res}
 
 
+def _graph_us(launches, reps=10):
+    """Mean microseconds per launch: the callables, each enqueueing one launch
+    on the current stream, captured once into a HIP graph that is replayed
+    `reps` times between two HIP events on the capturing stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in launches:
+            f()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for f in launches:
+                f()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for _ in range(reps):
+            g.replay()
+        b.record(s)
+        torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / (reps * len(launches))
+
+
+def _cpu_us(fn, reps=3):
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return round(best * 1e6, 1)
+
+
+def kernel_configs(eng, cpu=True):
+    """BASELINE configs 1, 2, 3b, 4a and 4b one kernel (or kernel pair) at a
+    time, as the decode step launches them.  Inputs are drawn on the CPU from
+    torch.Generator seed 0 in the listed order (config 3b reuses the model's
+    lm_head, the same shape and distribution); every timed graph rotates over
+    enough input copies to exceed the 256 MB MALL.  achieved = algorithmic
+    bytes per call / mean time per call.  With cpu=True each config is also
+    timed on the host cores: (i) explicit block dequant + fp32 matmul per call,
+    (ii) pre-dequantized fp32 weights (the oracle, as the checker's CPU path)."""
+    from qwen35_amd import abi, engine as eng_mod, ops, synth
+    if cpu:
+        from oracle import qwen35_oracle as orc
+        torch.set_num_threads(os.cpu_count() or 1)
+    L, dev, bf = eng.lib, "cuda", torch.bfloat16
+    st = lambda: abi.stream_handle()
+    g = torch.Generator().manual_seed(0)
+    res = []
+
+    def entry(name, kernel, nbytes, us, copies, cpu_times=None):
+        e = {"config": name, "kernel": kernel, "algorithmic_bytes": int(nbytes), "us": round(us, 3),
+             "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+        if cpu_times:
+            e["cpu_us"] = cpu_times
+            e["cpu_threads"] = torch.get_num_threads()
+        res.append(e)
+        log(f"{name}: {us:.2f} us, {e['GBps']} GB/s")
+
+    def gemv_launch(x, w, s, y, res1=None):
+        return lambda: abi.check(L.qh_gemv_e4m3(
+            abi.ptr(x), None, None, 1e-6, x.numel(), abi.ptr(res1), None, 1, abi.ptr(w), abi.ptr(s),
+            abi.ptr(y), w.shape[0], ops.scale_mode(w, s), *([None, None, None, 0, 0] * 3), 0, st()),
+            "gemv")
+
+    # ---- 1: single GEMV 9216 x 2560 -------------------------------------------
+    W1 = torch.randn(9216, 2560, generator=g) * 0.02
+    w1, s1 = synth.quantize_block_fp8(W1)
+    x1 = torch.randn(2560, generator=g).to(bf)
+    n = 16
+    dw = [(w1.to(dev), s1.to(dev)) for _ in range(n)]
+    dx, dy = x1.to(dev), torch.empty(9216, dtype=bf, device=dev)
+    us = _graph_us([gemv_launch(dx, w, s, dy) for w, s in dw])
+    nbytes = 9216 * 2560 + s1.numel() * 4 + 2560 * 2 + 9216 * 2
+    cpu_t = None
+    if cpu:
+        Wd = orc.dequant(w1, s1)
+        cpu_t = {"dequant_matmul": _cpu_us(lambda: x1.float() @ orc.dequant(w1, s1).t()),
+                 "matmul": _cpu_us(lambda: x1.float() @ Wd.t())}
+    entry("1 GEMV 9216x2560", "gemv_fast_kernel<5, 4>", nbytes, us, n, cpu_t)
+    del dw
+
+    # ---- 2: decode MLP (norm + gate/up + SiLU*up, then down + residual) -------
+    ln = torch.randn(2560, generator=g) * 0.02
+    Wg = torch.randn(9216, 2560, generator=g) * 0.02
+    Wu = torch.randn(9216, 2560, generator=g) * 0.02
+    Wdn = torch.randn(2560, 9216, generator=g) * 0.02
+    h = torch.randn(2560, generator=g).to(bf)
+    (wg, sg), (wu, su), (wd, sd) = (synth.quantize_block_fp8(W) for W in (Wg, Wu, Wdn))
+    sets = [tuple(t.to(dev) for t in (wg, sg, wu, su, wd, sd)) for _ in range(n)]
+    dh, dln = h.to(dev), ln.to(dev)
+    dm = torch.empty(9216, dtype=bf, device=dev)
+    dout = torch.empty(2560, dtype=bf, device=dev)
+    launches = []
+    for a_, b_, c_, d_, e_, f_ in sets:
+        launches.append(lambda a_=a_, b_=b_, c_=c_, d_=d_: abi.check(L.qh_mlp_gate_up(
+            abi.ptr(dh), None, abi.ptr(dln), 1e-6, 2560, abi.ptr(a_), abi.ptr(b_), abi.ptr(c_),
+            abi.ptr(d_), 9216, ops.scale_mode(a_, b_), abi.ptr(dm), None, None, 0, st()), "mlp"))
+        launches.append(gemv_launch(dm, e_, f_, dout, res1=dh))
+    us = _graph_us(launches) * 2            # per MLP call (two launches)
+    nbytes = (3 * 9216 * 2560 + (sg.numel() + su.numel() + sd.numel()) * 4
+              + 2560 * 2 + 2560 * 4 + 2 * 9216 * 2 + 2560 * 2 * 2)
+    cpu_t = None
+    if cpu:
+        mats = [orc.dequant(w, s) for w, s in ((wg, sg), (wu, su), (wd, sd))]
+        zero = torch.zeros(2560)
+
+        def mlp_dq():
+            m3 = [orc.dequant(w, s) for w, s in ((wg, sg), (wu, su), (wd, sd))]
+            orc.mlp_decode(h, zero, ln, *m3)
+        cpu_t = {"dequant_matmul": _cpu_us(mlp_dq),
+                 "matmul": _cpu_us(lambda: orc.mlp_decode(h, zero, ln, *mats))}
+    entry("2 MLP gate/up 9216x2560 x2 + down 2560x9216", "mlp_fast_kernel<5, 1> + gemv_fast_kernel<18, 1>",
+          nbytes, us, n, cpu_t)
+    del sets
+
+    # ---- 3b: lm_head (bf16 248320 x 2560) + greedy argmax -----------------------
+    Wl = eng.w.lm_head
+    V, K = Wl.shape
+    lx = torch.randn(K, generator=g).to(bf)
+    dlx = lx.to(dev)
+    logits = torch.empty(V, dtype=bf, device=dev)
+    scratch = torch.zeros(int(L.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8, device=dev)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    lm = lambda: abi.check(L.qh_lm_head_argmax(
+        abi.ptr(dlx), abi.ptr(eng.w.norm_f), 1e-6, K, abi.ptr(Wl), V, abi.ptr(logits),
+        abi.ptr(scratch), abi.ptr(counter), abi.ptr(tok), None, 0, None, None, None, st()), "lm_head")
+    us = _graph_us([lm] * 4, reps=5)
+    nbytes = V * K * 2 + K * 2 + K * 4 + V * 2
+    cpu_t = None
+    if cpu:
+        Wc = Wl.cpu()
+        Wf = Wc.float()
+        cpu_t = {"dequant_matmul": _cpu_us(lambda: lx.float() @ Wc.float().t(), reps=2),
+                 "matmul": _cpu_us(lambda: lx.float() @ Wf.t(), reps=2)}
+        del Wc, Wf
+    entry("3b lm_head 248320x2560 bf16 + argmax", "lm_head_argmax_kernel<5, 2>", nbytes, us, 1, cpu_t)
+
+    # ---- 4a: GatedDeltaNet decode step (conv + gates + l2norm + delta rule) -----
+    Hk, Hv, dk, dv = 16, 32, 128, 128
+    C = 2 * Hk * dk + Hv * dv
+    S = torch.randn(Hv, dk, dv, generator=g) * 0.1
+    qk = torch.randn(2 * Hk * dk, generator=g).to(bf)
+    vv = torch.randn(Hv * dv, generator=g).to(bf)
+    a_ = torch.randn(Hv, generator=g).to(bf)
+    b_ = torch.randn(Hv, generator=g).to(bf)
+    ring = (torch.randn(C, 4, generator=g) * 0.02).to(bf)
+    cw = (torch.randn(C, 4, generator=g) * 0.02).to(bf)
+    A_log = torch.log(1e-3 + torch.rand(Hv, generator=g) * 16)
+    dt = torch.ones(Hv)
+    mixed = torch.cat([qk, vv])
+    n4 = 128
+    dstate = [S.to(dev) for _ in range(n4)]
+    dring = [ring.to(dev) for _ in range(n4)]
+    dmix, da, db, dcw, dA, ddt = (t.to(dev) for t in (mixed, a_, b_, cw, A_log, dt))
+    core = torch.empty(Hv * dv, dtype=bf, device=dev)
+    gdn = [lambda s_=s_, r_=r_: abi.check(L.qh_gdn_decode_core(
+        abi.ptr(dmix), abi.ptr(da), abi.ptr(db), abi.ptr(r_), abi.ptr(dcw), abi.ptr(dA), abi.ptr(ddt),
+        abi.ptr(s_), abi.ptr(core), None, 7, Hk, Hv, dk, dv, st()), "gdn_core")
+        for s_, r_ in zip(dstate, dring)]
+    us = _graph_us(gdn, reps=5)
+    nbytes = 2 * Hv * dk * dv * 4 + 2 * C * 4 * 2 + C * 4 * 2 + C * 2 + Hv * 12 + Hv * dv * 2
+    cpu_t = None
+    if cpu:
+        def gdn_cpu():
+            stt = ring.float().clone()
+            y = orc.conv_update(mixed.float(), stt, cw.float())
+            q = y[:Hk * dk].view(Hk, dk).repeat_interleave(Hv // Hk, 0)
+            k = y[Hk * dk:2 * Hk * dk].view(Hk, dk).repeat_interleave(Hv // Hk, 0)
+            gg, beta = orc.linear_gates(a_.float(), b_.float(), A_log, dt)
+            orc.delta_rule_step(q, k, y[2 * Hk * dk:].view(Hv, dv), gg, beta, S.clone())
+        t_ = _cpu_us(gdn_cpu)
+        cpu_t = {"dequant_matmul": t_, "matmul": t_}
+    entry("4a GatedDeltaNet step (32 v-heads x 128 x 128 fp32 state)", "gdn_decode_cols_kernel",
+          nbytes, us, n4, cpu_t)
+    del dstate, dring
+
+    # ---- 4b: gated GQA decode attention at context 4096 ------------------------
+    H, KV, D, rot, ms = 16, 4, 256, 64, 4096
+    kc = torch.randn(KV, ms, D, generator=g).to(bf)
+    vc = torch.randn(KV, ms, D, generator=g).to(bf)
+    q = torch.randn(H, D, generator=g).to(bf)
+    gate = torch.randn(H, D, generator=g).to(bf)
+    kn = torch.randn(KV, D, generator=g).to(bf)
+    vn = torch.randn(KV, D, generator=g).to(bf)
+    qnw = torch.randn(D, generator=g) * 0.02
+    knw = torch.randn(D, generator=g) * 0.02
+    q_all = torch.cat([q, gate], dim=1).contiguous()
+    cos, sin = eng_mod.rope_tables(ms, rot, 1e7, device=dev)
+    nsplit = eng_mod.default_attn_splits(ms)
+    caches = [(kc.to(dev), vc.to(dev)) for _ in range(n)]
+    dq, dkn, dvn, dqn, dknw = (t.to(dev) for t in (q_all, kn, vn, qnw, knw))
+    scr = torch.empty(int(L.qh_attn_scratch_bytes(KV, nsplit, D)), dtype=torch.uint8, device=dev)
+    cnt = torch.zeros(KV, dtype=torch.int32, device=dev)
+    aout = torch.empty(H * D, dtype=bf, device=dev)
+    att = [lambda k_=k_, v_=v_: abi.check(L.qh_attn_decode(
+        abi.ptr(dq), 2 * D, abi.ptr(dq[:, D:]), 2 * D, abi.ptr(dkn), abi.ptr(dvn), abi.ptr(dqn),
+        abi.ptr(dknw), abi.ptr(cos), abi.ptr(sin), abi.ptr(k_), abi.ptr(v_), ms, D, rot, H, KV, None,
+        ms - 1, nsplit, abi.ptr(scr), abi.ptr(cnt), abi.ptr(aout), 1e-6, st()), "attn")
+        for k_, v_ in caches]
+    us = _graph_us(att, reps=5)
+    nbytes = 2 * KV * ms * D * 2 + (H * 2 * D + 2 * KV * D + H * D) * 2
+    cpu_t = None
+    if cpu:
+        kf, vf = kc.float(), vc.float()
+        cc, sc = (t.cpu() for t in eng_mod.rope_tables(ms, rot, 1e7))
+        t_ = _cpu_us(lambda: orc.attn_decode(q_all.reshape(-1), kn, vn, qnw, knw, cc, sc, kf.clone(),
+                                             vf.clone(), ms - 1, H, KV, D, rot))
+        cpu_t = {"dequant_matmul": t_, "matmul": t_}
+    entry(f"4b attention 16Q/4KV x 256, context {ms}", "attn_decode_kernel<256>", nbytes, us, n, cpu_t)
+    del caches
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
     """CPU oracle decode on the host cores.  Returns (tok/s over the timed
     greedy steps, threads, setup seconds, prompt, oracle tokens, oracle logits
@@ -270,6 +493,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only time BASELINE configs 1-4 kernel by kernel (and on the CPU)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run the batch prefill of the bench prompt 3 times (for rocprofv3)")
     ap.add_argument("--prefill-gemm-probe", action="store_true",
@@ -305,6 +530,9 @@ def main():
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
     if args.traffic_probe:
         traffic_probe(eng)
+        return
+    if args.kernels_only:
+        print(json.dumps({"kernels": kernel_configs(eng, cpu=not args.no_cpu_baseline)}))
         return
     if args.prefill_probe:
         prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
@@ -348,6 +576,7 @@ def main():
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
     prefill = time_prefill(eng, prompt)
     log(f"prefill: {prefill['prompt_tokens']} tokens in {prefill['ms']} ms")
+    kernels = kernel_configs(eng, cpu=not args.no_cpu_baseline)
     gemm = time_prefill_gemm()
     log("prefill GEMM: " + ", ".join(f"{g['N']}x{g['K']} {g['us']} us ({g['tflops']} TFLOP/s)"
                                      for g in gemm["gemms"]))
@@ -412,6 +641,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "prefill_gemm": gemm,
+        "kernels": kernels,
         "parity": parity,
     }
     print(json.dumps(out))
