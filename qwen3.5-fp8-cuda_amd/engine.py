@@ -45,7 +45,11 @@ def rope_tables(max_pos, rotary_dim, theta, device="cpu"):
 
 
 def default_attn_splits(max_seq):
-    return max(1, min(32, max_seq // 128))
+    """Position splits of the decode attention: 64 for a 4096-position cache.
+    A split spans one 32-position tile up to 2048 positions, so short contexts
+    run the same active splits whatever the count; at context 4096, 64 splits
+    (256 workgroups, 2 tiles each) measured 21.4 us against 22.8 us with 32."""
+    return max(1, min(64, max_seq // 64))
 
 
 class Qwen35FP8Engine:
