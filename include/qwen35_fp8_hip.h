@@ -263,7 +263,10 @@ int qh_gemv_e4m3_gated(const void* core, const void* z, const void* norm_w, int 
                        const void* res, const void* w, const void* s, void* y, int n, int kb,
                        int scales_bf16, qh_stream_t stream);
 
-/* Workspace bytes for qh_gemm_e4m3. */
+/* Workspace bytes for qh_gemm_e4m3 / qh_gemm_e4m3_grouped with M rows of K:
+ * the activation's hi and lo E4M3 terms (2 M K bytes), the row scales and a
+ * fixed 16 MiB region for split-K partials.  Calls sharing a workspace must
+ * not overlap. */
 size_t qh_gemm_workspace_size(int M, int K);
 
 /* Prefill GEMM on the fp8 matrix cores (fp8_gemm_batch semantics). */
