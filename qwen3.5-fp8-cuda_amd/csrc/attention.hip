@@ -124,7 +124,7 @@ __device__ __forceinline__ void norm_rope(float (&v)[D / 64], bool has_norm, con
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) ss = fmaf(v[i], v[i], ss);
-    ss = wave_sum(ss);
+    ss = wave_total(ss);
     const float rs = rsqrtf(ss / (float)D + eps);
 #pragma unroll
     for (int i = 0; i < NPL; ++i) v[i] = rbf(v[i] * rs * (1.0f + nw[i]));
@@ -307,11 +307,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
         }
         dot += __shfl_xor(dot, 1, 64);
         const float s = valid ? dot * scale : -INFINITY;
-        const float tmax = wave_max(s);
+        const float tmax = wave_max_dpp(s);
         const float nm = fmaxf(m[hi], tmax);
         const float corr = __expf(m[hi] - nm);
         const float pv = valid ? __expf(s - nm) : 0.0f;
-        const float psum = wave_sum(half == 0 ? pv : 0.0f);
+        const float psum = wave_total(half == 0 ? pv : 0.0f);
         l[hi] = l[hi] * corr + psum;
         m[hi] = nm;
         if (half == 0) sP[gi][prow] = pv;
@@ -391,9 +391,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
 #pragma unroll
     for (int u = 0; u < MB; ++u)
       load_head_f32_coherent<NPL>(part[u], base + (size_t)u * sstride, lane, u < nactive);
-    const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
+    const float M = wave_max_dpp(ls > 0.0f ? ms : -INFINITY);
     const float ws = ls > 0.0f ? __expf(ms - M) : 0.0f;
-    const float L = wave_sum(ls * ws);
+    const float L = wave_total(ls * ws);
     float acc[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
