@@ -140,11 +140,12 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 // Block-wide sum for an NT-thread block; `red` must hold >= NT/64 floats of LDS.
+// One barrier: the caller must pass a workgroup barrier after reading the
+// result and before the next block_sum / block_sum_256 on the same `red`.
 template <int NT>
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  __syncthreads();
   if (lane == 0) red[wid] = v;
   __syncthreads();
   float s = 0.0f;
@@ -154,10 +155,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // Block-wide sum for a 256-thread block; `red` must hold >= 4 floats of LDS.
+// Same single-barrier contract as block_sum.
 __device__ __forceinline__ float block_sum_256(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  __syncthreads();
   if (lane == 0) red[wid] = v;
   __syncthreads();
   return red[0] + red[1] + red[2] + red[3];
