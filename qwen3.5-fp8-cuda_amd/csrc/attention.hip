@@ -38,6 +38,24 @@ __device__ __forceinline__ void load_head(float (&v)[NPL], const uint16_t* src) 
   }
 }
 
+// load_head through a buffer resource, for loads that would otherwise sit
+// under a branch (the compiler then waits for every earlier load there):
+// valid == false gives an empty resource, whose load reads zeros.  `valid`
+// must be wave-uniform.
+template <int NPL>
+__device__ __forceinline__ void load_head_b(float (&v)[NPL], const uint16_t* head, int lane, bool valid) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(head), (short)0, valid ? (int)(64 * NPL * 2) : 0, 0x00020000);
+  const uint32_t off = (uint32_t)lane * NPL * 2u;
+  if constexpr (NPL == 4) {
+    const u32x2 u = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    v[0] = bf_lo(u.x); v[1] = bf_hi(u.x); v[2] = bf_lo(u.y); v[3] = bf_hi(u.y);
+  } else {
+    const uint32_t u = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    v[0] = bf_lo(u); v[1] = bf_hi(u);
+  }
+}
+
 template <int NPL>
 __device__ __forceinline__ void store_head(uint16_t* dst, const float (&v)[NPL]) {
   if constexpr (NPL == 4) {
@@ -95,11 +113,19 @@ struct NormRopeIn {
 template <int NPL>
 __device__ __forceinline__ void load_norm_w(NormRopeIn<NPL>& in, const float* q_norm_w,
                                             const float* k_norm_w, int lane) {
+  // Buffer loads keep this branch-free (a load under a branch makes the
+  // compiler wait for every earlier load there): a null pointer gets an empty
+  // resource, whose loads read 0.
+  constexpr int bytes = NPL * 64 * 4;
+  const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(q_norm_w), (short)0,
+                                                    q_norm_w ? bytes : 0, 0x00020000);
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(k_norm_w), (short)0,
+                                                    k_norm_w ? bytes : 0, 0x00020000);
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
-    const int c = lane * NPL + i;
-    in.qw[i] = q_norm_w ? q_norm_w[c] : 0.0f;
-    in.kw[i] = k_norm_w ? k_norm_w[c] : 0.0f;
+    const int off = (lane * NPL + i) * 4;
+    in.qw[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, off, 0, 0));
+    in.kw[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rk, off, 0, 0));
   }
 }
 template <int NPL>
@@ -169,19 +195,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
     const int gi = wid + 4 * hi;
-    if (gi < G) {
-      load_head<NPL>(qraw[hi], p.q + (size_t)(kvh * G + gi) * p.q_stride + lane * NPL);
-      if (p.gate)
-        load_head<NPL>(gate_v[hi], p.gate + (size_t)(kvh * G + gi) * p.gate_stride + lane * NPL);
-    }
+    const bool ok = gi < G;
+    const size_t h = (size_t)(kvh * G + (ok ? gi : 0));
+    load_head_b<NPL>(qraw[hi], p.q + h * p.q_stride, lane, ok);
+    load_head_b<NPL>(gate_v[hi], p.gate ? p.gate + h * p.gate_stride : nullptr, lane,
+                     ok && p.gate != nullptr);
   }
   float kraw[NPL], vraw[NPL];
-  if (wid == 0 && p.k_new) {
-    load_head<NPL>(kraw, p.k_new + (size_t)kvh * D + lane * NPL);
-    load_head<NPL>(vraw, p.v_new + (size_t)kvh * D + lane * NPL);
-  }
+  const bool kv_in = wid == 0 && p.k_new != nullptr;
+  load_head_b<NPL>(kraw, kv_in ? p.k_new + (size_t)kvh * D : nullptr, lane, kv_in);
+  load_head_b<NPL>(vraw, kv_in ? p.v_new + (size_t)kvh * D : nullptr, lane, kv_in);
   NormRopeIn<NPL> nr;
   load_norm_w<NPL>(nr, p.q_norm_w, p.k_norm_w, lane);
+
+  const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
+  const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
+  // K/V tile staging: each thread moves PER 16-byte pieces of K and of V.
+  // Loads are branch-free (rows at or past `lim` are clamped to row t0, and
+  // lim <= max_seq) so a whole tile is in flight at once; the next tile is
+  // requested before the current one is used.
+  constexpr int PER = TP * (D / 8) / 256;
+  u32x4 kreg[PER], vreg[PER];
+  auto fetch = [&](int t0, int lim) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int idx = threadIdx.x + 256 * e;
+      const int pos = t0 + idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const int src = pos < lim ? pos : t0;
+      kreg[e] = *(const u32x4*)(kbase + (size_t)src * D + c8);
+      vreg[e] = *(const u32x4*)(vbase + (size_t)src * D + c8);
+    }
+  };
+  auto span_of = [&](int n) {
+    const int s = (n + p.nsplit - 1) / p.nsplit;
+    return ((s + TP - 1) / TP) * TP;
+  };
 
   int rope_pos = p.rope_pos, slot = p.slot, total = p.total;
   if (p.pos_dev) {
@@ -192,8 +241,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   }
   // A device-resident position past the cache touches nothing (bounds guard).
   if (slot < 0 || slot >= p.max_seq || total > p.max_seq) return;
-  int span = (total + p.nsplit - 1) / p.nsplit;
-  span = ((span + TP - 1) / TP) * TP;
+  // The span is sized to the context.  (A span fixed by the cache length,
+  // whose first tile can be requested before the position arrives, leaves
+  // fewer active splits at short context and measured slower.)
+  const int span = span_of(total);
   const int p0 = split * span;
   const int p1 = min(total, p0 + span);
   // Splits past the context do nothing and do not take part in the merge:
@@ -207,26 +258,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   const float* cos_row = p.cos_t + (size_t)rope_pos * p.rot;
   const float* sin_row = p.sin_t + (size_t)rope_pos * p.rot;
   const float scale = rsqrtf((float)D);
-  const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
-  const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
   const bool new_kv = p.k_new != nullptr;
 
-  // K/V tile staging: each thread moves PER 16-byte pieces of K and of V.
-  // Loads are branch-free (clamped to a valid row) so a whole tile is in
-  // flight at once; the next tile is requested before the current one is used.
-  constexpr int PER = TP * (D / 8) / 256;
-  u32x4 kreg[PER], vreg[PER];
-  auto fetch = [&](int t0) {
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int idx = threadIdx.x + 256 * e;
-      const int pos = t0 + idx / (D / 8);
-      const int c8 = (idx % (D / 8)) * 8;
-      const int src = pos < p1 ? pos : t0;
-      kreg[e] = *(const u32x4*)(kbase + (size_t)src * D + c8);
-      vreg[e] = *(const u32x4*)(vbase + (size_t)src * D + c8);
-    }
-  };
   auto stage = [&](int t0) {
     const u32x4 zero = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -245,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
       *(u32x4*)(sV + row * D + c8) = vq;
     }
   };
-  if (p0 < p1) fetch(p0);
+  if (p0 < p1) fetch(p0, p1);
   load_rope<NPL>(nr, cos_row, sin_row, p.rot, lane);
 
   // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
@@ -286,7 +319,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   for (int t0 = p0; t0 < p1; t0 += TP) {
     stage(t0);
     __syncthreads();
-    if (t0 + TP < p1) fetch(t0 + TP);
+    if (t0 + TP < p1) fetch(t0 + TP, p1);
 
     // scores: lane pair (2j, 2j+1) owns position t0+j, each lane half the dims
     const int prow = lane >> 1, half = lane & 1;
