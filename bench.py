@@ -159,11 +159,9 @@ def prefill_gemm_launchers(inputs):
         M, K = x.shape
         N = w.shape[0]
         y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-        ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device="cuda")
-
-        def run(x=x, w=w, s=s, y=y, ws=ws, M=M, N=N, K=K):
+        def run(x=x, w=w, s=s, y=y, M=M, N=N, K=K):
             abi.check(lib.qh_gemm_e4m3(abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M, N, K,
-                                       K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm")
+                                       K // 128, 0, None, abi.stream_handle()), "gemm")
         out.append(((M, N, K), run))
     return out
 
@@ -205,8 +203,9 @@ def time_prefill_gemm(reps=20):
                     "frac_fp8_dense_peak": round(tf / FP8_MFMA_PEAK_TFLOPS, 4)})
     return {"config": "BASELINE configs[2]: X[512x2560] x W[9216x2560]^T and X'[512x9216] x "
                       "W'[2560x9216]^T, E4M3 128x128 block scales, seed 0",
-            "kernel": "quant_rows_kernel + gemm_e4m3_lds_kernel (v_mfma_scale_f32_32x32x64_f8f6f4; "
-                      "activation as hi+lo E4M3 terms: two fp8 products per multiply-add)",
+            "kernel": "gemm_e4m3_lds_kernel (v_mfma_scale_f32_32x32x64_f8f6f4; the bf16 activation "
+                      "split in-tile into hi+lo E4M3 terms with per-(row, 32-K) E8M0 run scales: "
+                      "two fp8 products per multiply-add, no workspace)",
             "peak_tflops": FP8_MFMA_PEAK_TFLOPS, "gemms": res}
 
 

@@ -9,9 +9,7 @@
 //   2. Native `qh_*` entry points used by this framework's host: fp32
 //      scale_inv, device-resident positions for HIP-graph replay, fused
 //      epilogues; they return 0 on success and -1 with qh_last_error() set.
-// Every buffer is caller-owned device memory.  The one exception is the
-// reference's fp8_gemm_batch, which passes no workspace: the prefill GEMM then
-// keeps one internal, grow-on-demand activation buffer (gemm.hip).
+// Every buffer is caller-owned device memory; the library allocates nothing.
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -661,7 +659,8 @@ QH_EXPORT size_t qh_sample_workspace_size(int V) { return qh_sample_workspace_by
 
 // Nucleus sampling of one bf16 logits row (main.py:49-87) on the device.
 QH_EXPORT int qh_sample_top_p(const void* logits, int V, float temperature, float top_p,
-                              float rep_penalty, int64_t* hist, const int* pos_dev, int pos,
+                              float rep_penalty, int64_t* hist, int hist_len,
+                              const int* pos_dev, int pos,
                               int pos_offset, const int* lo_dev, int window, uint64_t seed,
                               uint64_t* counter, void* ws, int64_t* tok_out, const void* embed,
                               void* h, int D, int64_t* info, hipStream_t stream) {
@@ -673,6 +672,7 @@ QH_EXPORT int qh_sample_top_p(const void* logits, int V, float temperature, floa
   p.top_p = top_p;
   p.rep_penalty = rep_penalty;
   p.hist = hist;
+  p.hist_len = hist_len;
   p.pos_dev = pos_dev;
   p.pos = pos;
   p.pos_offset = pos_offset;
@@ -722,8 +722,8 @@ QH_EXPORT int qh_gated_rmsnorm(const void* core, const void* z, const void* w, v
 QH_EXPORT size_t qh_gemm_workspace_size(int M, int K) { return qh_gemm_workspace_bytes(M, K); }
 
 // Prefill block-scaled E4M3 GEMM: Y[M,N] = bf16(X[M,K] . deq(W)[N,K]^T) on the
-// fp8 matrix cores.  `ws` (qh_gemm_workspace_size bytes) holds the split
-// activations; when null the library uses an internal buffer.
+// fp8 matrix cores.  `ws` (qh_gemm_workspace_size bytes, optional) holds
+// split-K partials; without it the GEMM does not split K.
 QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N,
                            int K, int kb, int scales_bf16, void* ws, hipStream_t stream) {
   if (!k_ok(K, "qh_gemm_e4m3")) return -1;
@@ -738,7 +738,7 @@ QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y,
 // projection as its own fp8_gemm_batch, main.py:262-269).  Up to 4
 // projections of the same activation X[M, K] -- segment t:
 // Y_t[M, n_t] = bf16(X . deq(W_t)^T), scale mode kb_t -- with one activation
-// split and one launch.  `ws` as for qh_gemm_e4m3.
+// split and one launch.  `ws` as for qh_gemm_e4m3 (optional).
 QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0,
                                    const void* s0, void* y0, int n0, int kb0, const void* w1,
                                    const void* s1, void* y1, int n1, int kb1, const void* w2,
@@ -746,8 +746,8 @@ QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const 
                                    const void* s3, void* y3, int n3, int kb3, int scales_bf16,
                                    void* ws, hipStream_t stream) {
   if (!k_ok(K, "qh_gemm_e4m3_grouped")) return -1;
-  if (!x || !ws) {
-    qh_set_error("qh_gemm_e4m3_grouped: null activation or workspace");
+  if (!x) {
+    qh_set_error("qh_gemm_e4m3_grouped: null activation");
     return -1;
   }
   if (M <= 0) return 0;

@@ -4,99 +4,106 @@
 // fp8_gemm_batch_kernel; caller main.py:262-269):
 //   Y[m, n] = bf16( sum_kb s[n, kb] * sum_{k in kb} X[m, k] * e4m3(W[n, k]) )
 //
-// The activations are bf16, the matrix cores take E4M3 on both sides, so X is
-// split into two E4M3 terms per row: with s_x = max|X[m,:]| / 448,
-//   hi = e4m3(X / s_x),  lo = e4m3(X / s_x - hi),  X ~= s_x * (hi + lo)
-// (about 8 significant bits, like bf16).  Both terms meet the same W tile in
-// v_mfma_scale_f32_32x32x64_f8f6f4 (E4M3 operands, its MX block-scale operands
-// fixed at 2^0) and accumulate into one per-K-block partial, which is scaled by
-// the W block scale and added to the fp32 accumulator; the row scale s_x is
-// applied once in the epilogue.
+// The activations are bf16 and the matrix cores take E4M3 on both sides, so
+// each 32-element run of a row of X (one MX block of the matrix-core
+// instruction) is split into two E4M3 terms while the A tile is staged:
+//   E = floor(log2 max|x|) - 7 over the run (a power of two, E8M0),
+//   hi = e4m3(x / 2^E),  lo = e4m3((x / 2^E - hi) * 16),
+//   x = 2^E hi + 2^(E - 4) lo.
+// A bf16 value has 8 significant bits; hi keeps the top 4 (rounded) and the
+// remainder has at most 4, so the split is exact for every element within
+// 2^13 of its run's maximum (smaller ones keep an absolute error below
+// 2^-21 of that maximum).  A channel 1000x larger than its neighbours
+// therefore costs the neighbours nothing.  Both terms meet the same W tile in
+// v_mfma_scale_f32_32x32x64_f8f6f4 with their run exponents as the per-lane
+// E8M0 A scales (W's scale operand fixed at 2^0), products are exact in fp32,
+// and each 128-wide K block's partial is multiplied by the weight block scale
+// and added to the fp32 accumulator.
 //
-// Tiling: BM x BN output tile per 256-thread workgroup (64x64, or 128x128 when
-// there are enough tiles), a 2 x 2 grid of waves each holding (BM/2) x (BN/2)
-// of 32x32 matrix-core tiles.  Each 128-wide K block of A hi, A lo and B is
-// staged once per workgroup in LDS (rows padded to 144 bytes against bank
-// conflicts, one or two stages), the next one or two blocks in registers
-// while the current one is multiplied.  Within a K block, lane half h of a 32x32x64 instruction
-// takes bytes [64q + 32h, +32) of its row in both operands: the same K
-// permutation on A and B leaves the contraction unchanged.
-#include <mutex>
-
+// Nothing is precomputed: no activation pass, no workspace.  A caller
+// workspace only enables split-K (qh_gemm_e4m3 / qh_gemm_e4m3_grouped); the
+// reference entry point fp8_gemm_batch passes none and never splits.
+//
+// Tiling: 64 x BN output tile per 256-thread workgroup (BN = 64, or 128 when
+// that still gives two tiles per CU), a 2 x 2 grid of waves each holding
+// 32 x (BN/2) of 32x32 matrix-core tiles.  Each 128-wide K block of A hi, A lo
+// and B is staged once per workgroup in LDS (rows padded to 144 bytes against
+// bank conflicts, one or two stages), the next one or two blocks in registers
+// while the current one is multiplied.  Operand layout of the 32x32x64
+// instruction (measured on gfx950 with one-hot operands and distinct
+// per-lane scales): lane (r, h) holds 32 bytes of row r, and its bytes 0-15
+// belong to MX block 0 (scaled by lane r's scale byte), bytes 16-31 to block
+// 1 (lane r + 32's).  So for the q-th 64-byte chunk of a K block, lane half h
+// takes bytes [64q + 16h, +16) and [64q + 32 + 16h, +16) of its row in both
+// operands: block 0 is run 2q, block 1 run 2q + 1, and lane half h supplies
+// run 2q + h's exponent.
 #include "qh_common.h"
 #include "qh_gemm.h"
 
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
-
-__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* x, uint8_t* xhi,
-                                                         uint8_t* xlo, float* sx, int K) {
-  __shared__ float red[4];
-  const int row = blockIdx.x;
-  const uint16_t* xr = x + (size_t)row * K;
-  float amax = 0.0f;
-  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    const u32x4 v = *(const u32x4*)(xr + k);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(bf_lo(v.x)), fabsf(bf_hi(v.x))),
-                             fmaxf(fabsf(bf_lo(v.y)), fabsf(bf_hi(v.y)))));
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(bf_lo(v.z)), fabsf(bf_hi(v.z))),
-                             fmaxf(fabsf(bf_lo(v.w)), fabsf(bf_hi(v.w)))));
-  }
-  amax = wave_max(amax);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
-  const float inv = 1.0f / s;
-  if (threadIdx.x == 0) sx[row] = s;
-  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    const u32x4 v = *(const u32x4*)(xr + k);
-    float f[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
-                  bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
-    uint32_t hi[2], lo[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      float a[4], r[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a[e] = fminf(fmaxf(f[4 * q + e] * inv, -448.0f), 448.0f);
-      uint32_t h = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0u, false);
-      h = __builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], h, true);
-      const qh_f32x2 h01 = e4m3x2_lo_f32(h), h23 = e4m3x2_hi_f32(h);
-      r[0] = a[0] - h01.x; r[1] = a[1] - h01.y; r[2] = a[2] - h23.x; r[3] = a[3] - h23.y;
-      uint32_t l = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0u, false);
-      l = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], l, true);
-      hi[q] = h;
-      lo[q] = l;
-    }
-    *(u32x2*)(xhi + (size_t)row * K + k) = u32x2{hi[0], hi[1]};
-    *(u32x2*)(xlo + (size_t)row * K + k) = u32x2{lo[0], lo[1]};
-  }
-}
-
-// gfx950 variant: operands staged through LDS once per workgroup (the four
-// waves of a tile share its A and B rows), the next K blocks loaded into
-// registers while the current one is multiplied, and the 32x32x64 fp8
-// matrix-core instruction (its block-scale operands fixed at 2^0: the
-// checkpoint's fp32 block scale is applied per 128-wide K block in fp32).
-// A, A_lo and B rows of a K block are 128 bytes; LDS rows are padded to 144
-// bytes so the 32 rows a lane group reads at one column land in distinct banks.
 typedef int v8i __attribute__((ext_vector_type(8)));
 constexpr int kGRow = 144;                      // padded LDS row (bytes)
+constexpr int kBM = 64;                         // output rows per tile
 
-__device__ __forceinline__ v8i lds_v8(const uint8_t* p) {
-  const u32x4 a = *(const u32x4*)p, b = *(const u32x4*)(p + 16);
+// The two 16-byte K chunks a lane feeds the 32x32x64 instruction: bytes
+// [0, 16) at p, [16, 32) at p + 32.
+__device__ __forceinline__ v8i lds_operand(const uint8_t* p) {
+  const u32x4 a = *(const u32x4*)p, b = *(const u32x4*)(p + 32);
   return v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
-// LDS bytes of one K-block stage of a BM x BN tile: A hi, A lo (BM rows), B
-// (BN rows), then the BN fp32 weight scales of the block.
-constexpr int gemm_stage_bytes(int bm, int bn) { return (2 * bm + bn) * kGRow + bn * 4; }
+// Split of one 32-element bf16 run (16 packed words) into E4M3 hi and lo
+// terms (32 bytes each) and the run's E8M0 exponent byte s of the hi term
+// (the lo term's is s - 4).  s = biased exponent of max|x| - 7, kept in
+// [4, 247]: then 2^(127 - s) is a normal fp32 and x * 2^(127 - s) < 256 (no
+// saturation); an all-zero run gives zero terms.
+__device__ __forceinline__ void split_run(const u32x4 (&v)[4], u32x4 (&hi)[2], u32x4 (&lo)[2],
+                                          uint32_t& s) {
+  float f[32];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    f[8 * c + 0] = bf_lo(v[c].x); f[8 * c + 1] = bf_hi(v[c].x);
+    f[8 * c + 2] = bf_lo(v[c].y); f[8 * c + 3] = bf_hi(v[c].y);
+    f[8 * c + 4] = bf_lo(v[c].z); f[8 * c + 5] = bf_hi(v[c].z);
+    f[8 * c + 6] = bf_lo(v[c].w); f[8 * c + 7] = bf_hi(v[c].w);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(f[e]));
+  const int ex = (int)((__float_as_uint(amax) >> 23) & 0xFFu);
+  s = (uint32_t)min(max(ex - 7, 4), 247);
+  const float inv = __uint_as_float((254u - s) << 23);    // 2^(127 - s)
+  uint32_t h[8], l[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    float a[4], r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = f[4 * q + e] * inv;
+    uint32_t hp = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0u, false);
+    hp = __builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], hp, true);
+    const qh_f32x2 h01 = e4m3x2_lo_f32(hp), h23 = e4m3x2_hi_f32(hp);
+    r[0] = (a[0] - h01.x) * 16.0f; r[1] = (a[1] - h01.y) * 16.0f;
+    r[2] = (a[2] - h23.x) * 16.0f; r[3] = (a[3] - h23.y) * 16.0f;
+    uint32_t lp = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0u, false);
+    lp = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], lp, true);
+    h[q] = hp;
+    l[q] = lp;
+  }
+  hi[0] = u32x4{h[0], h[1], h[2], h[3]};
+  hi[1] = u32x4{h[4], h[5], h[6], h[7]};
+  lo[0] = u32x4{l[0], l[1], l[2], l[3]};
+  lo[1] = u32x4{l[4], l[5], l[6], l[7]};
+}
 
-// NST LDS stages (1 or 2) and D K blocks in flight in registers.  The K loop
-// is unrolled by D so the register sets rotate statically; loads past the
-// last block re-read it (no branch, so the in-order load counter waits only
-// for the block about to be stored).  Requires (K / 128) % D == 0.
+// LDS of one K-block stage of a 64 x BN tile: A hi, A lo (64 rows), B (BN
+// rows), the BN fp32 weight scales of the block, then the 64 rows' four run
+// exponent bytes.
+constexpr int gemm_scw_off(int bn) { return (2 * kBM + bn) * kGRow; }
+constexpr int gemm_sca_off(int bn) { return gemm_scw_off(bn) + bn * 4; }
+constexpr int gemm_stage_bytes(int bn) { return gemm_sca_off(bn) + kBM * 4; }
+
 // Up to four projections of the same activation in one launch: segment t
 // owns N tiles [tstart[t], tstart[t + 1]) of the grid's x dimension.
 struct GemmGroup {
@@ -109,19 +116,23 @@ struct GemmGroup {
   int nseg;
 };
 
-template <typename ScaleT, int BM, int BN, int NST, int D>
-// Split-K (part != null): blockIdx.z takes K blocks [z KB/S, (z+1) KB/S) of
-// S = gridDim.z and stores its fp32 partial tile, unscaled, at
-// part[(z M + m) ldp + global column]; gemm_splitk_reduce_kernel finishes.
-__global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, const uint8_t* xlo,
-                                                            const float* sx, GemmGroup g, int M,
+// NST LDS stages (1 or 2) and D K blocks in flight in registers.  The K loop
+// is unrolled by D so the register sets rotate statically; loads past the
+// last block re-read it (no branch, so the in-order load counter waits only
+// for the block about to be stored).  Requires (K / 128 / gridDim.z) % D == 0.
+// Split-K (part != null): blockIdx.z takes K blocks [z KB, (z+1) KB) and
+// stores its fp32 partial tile at part[(z M + m) ldp + global column];
+// gemm_splitk_reduce_kernel finishes.
+template <typename ScaleT, int BN, int NST, int D>
+__global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint16_t* x, GemmGroup g, int M,
                                                             int K, float* part, int ldp) {
+  constexpr int BM = kBM;
   constexpr int WM = BM / 2, WN = BN / 2;        // this wave's sub-tile (2 x 2 waves)
-  constexpr int TI = WM / 32, TJ = WN / 32;      // 32x32 matrix-core tiles per wave
-  constexpr int STAGE = gemm_stage_bytes(BM, BN);
-  constexpr int PIECES = (2 * BM + BN) * 8;      // 16-byte pieces per K block
-  constexpr int PPT = PIECES / 256;              // per thread
-  static_assert(PIECES % 256 == 0 && TI >= 1 && TJ >= 1 && (NST == 1 || NST == 2), "tile shape");
+  constexpr int TJ = WN / 32;                    // 32x32 matrix-core tiles per wave
+  constexpr int STAGE = gemm_stage_bytes(BN);
+  constexpr int SCW = gemm_scw_off(BN), SCA = gemm_sca_off(BN);
+  constexpr int BPT = BN * 8 / 256;              // 16-byte W pieces per thread
+  static_assert(WM == 32 && TJ >= 1 && BPT >= 1 && (NST == 1 || NST == 2), "tile shape");
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -140,96 +151,99 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
   const int r = lane & 31, h = lane >> 5;
   const int KB = K / 128 / (int)gridDim.z;        // K blocks of this workgroup
   const int kb0 = (int)blockIdx.z * KB;
+  // Thread t stages MX run (t & 3) of tile row t >> 2 (64 bf16 bytes) and W
+  // pieces t + 256 e (row p >> 3, 16-byte column p & 7).  Rows past M or N
+  // re-read the last one (their results are never stored).
+  const int arow = tid >> 2, arun = tid & 3;
+  const uint16_t* xa = x + (size_t)min(mb + arow, M - 1) * K + 32 * arun;
 
-  // Global -> register staging: piece p is (operand row, 16-byte column) of
-  // the stage's rows [A hi (BM) | A lo (BM) | B (BN)].
   // The block's weight scales travel with its operands and are staged in LDS
   // beside them: a scale loaded at use time would sit behind every prefetched
-  // block in the in-order load counter and drain the pipeline at each K step.
-  // Thread t loads the scale of tile column t % BN (every thread loads, so no
-  // load sits under a branch).
-  constexpr int SC_OFF = (2 * BM + BN) * kGRow;
-  u32x4 st[D][PPT];
+  // block in the in-order load counter.  Thread t loads the scale of tile
+  // column t % BN (every thread loads, so no load sits under a branch).
+  u32x4 sa[D][4], sb[D][BPT];
   float scv[D];
-  auto gload = [&](u32x4 (&dst)[PPT], float& sdst, int kb) {
+  auto gload = [&](u32x4 (&da)[4], u32x4 (&db)[BPT], float& sdst, int kb) {
     kb = kb0 + min(kb, KB - 1);
     const int ko = kb * 128;
     sdst = load_scale<ScaleT>(sw, scale_index(kb_code, min(nb + tid % BN, N - 1), kb));
 #pragma unroll
-    for (int e = 0; e < PPT; ++e) {
+    for (int c = 0; c < 4; ++c) da[c] = *(const u32x4*)(xa + ko + 8 * c);
+#pragma unroll
+    for (int e = 0; e < BPT; ++e) {
       const int piece = tid + 256 * e;
-      const int row = piece >> 3, c16 = (piece & 7) * 16;
-      if (row < 2 * BM) {
-        const int m = min(mb + (row % BM), M - 1);
-        dst[e] = *(const u32x4*)((row < BM ? xhi : xlo) + (size_t)m * K + ko + c16);
-      } else {
-        const int n = min(nb + row - 2 * BM, N - 1);
-        dst[e] = __builtin_nontemporal_load((const u32x4*)(w + (size_t)n * K + ko + c16));
-      }
+      const int n = min(nb + (piece >> 3), N - 1);
+      db[e] = __builtin_nontemporal_load((const u32x4*)(w + (size_t)n * K + ko + (piece & 7) * 16));
     }
   };
-  auto sstore = [&](uint8_t* stage, const u32x4 (&src)[PPT], float sc) {
+  auto sstore = [&](uint8_t* stage, const u32x4 (&da)[4], const u32x4 (&db)[BPT], float sc) {
+    u32x4 hi[2], lo[2];
+    uint32_t s;
+    split_run(da, hi, lo, s);
+    uint8_t* ah = stage + arow * kGRow + 32 * arun;
+    uint8_t* al = stage + (BM + arow) * kGRow + 32 * arun;
+    *(u32x4*)ah = hi[0];
+    *(u32x4*)(ah + 16) = hi[1];
+    *(u32x4*)al = lo[0];
+    *(u32x4*)(al + 16) = lo[1];
+    stage[SCA + arow * 4 + arun] = (uint8_t)s;
 #pragma unroll
-    for (int e = 0; e < PPT; ++e) {
+    for (int e = 0; e < BPT; ++e) {
       const int piece = tid + 256 * e;
-      *(u32x4*)(stage + (piece >> 3) * kGRow + (piece & 7) * 16) = src[e];
+      *(u32x4*)(stage + (2 * BM + (piece >> 3)) * kGRow + (piece & 7) * 16) = db[e];
     }
-    if (tid < BN) *(float*)(stage + SC_OFF + tid * 4) = sc;
+    if (tid < BN) *(float*)(stage + SCW + tid * 4) = sc;
   };
 
-  v16f acc[TI][TJ];
+  v16f acc[TJ];
 #pragma unroll
-  for (int i = 0; i < TI; ++i)
+  for (int j = 0; j < TJ; ++j)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
 
   auto mma_block = [&](const uint8_t* cur) {
     float swj[TJ];
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) swj[j] = *(const float*)(cur + SC_OFF + (wn + 32 * j + r) * 4);
-    v16f t[TI][TJ];
+    for (int j = 0; j < TJ; ++j) swj[j] = *(const float*)(cur + SCW + (wn + 32 * j + r) * 4);
+    // this lane's run exponents: byte 0 -> run h (q = 0), byte 2 -> run 2 + h
+    // (q = 1); the lo term's are 4 lower (every byte >= 4: no borrow).  The
+    // instruction reads byte 0 of its scale operand whatever OPSEL says, so
+    // run 2 + h is shifted down for q = 1.
+    const uint32_t ws_hi = *(const uint32_t*)(cur + SCA + (wm + r) * 4) >> (8 * h);
+    const uint32_t ws_lo = ws_hi - 0x04040404u;
+    v16f t[TJ];
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) t[i][j][e] = 0.0f;
+      for (int e = 0; e < 16; ++e) t[j][e] = 0.0f;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      // lane half h takes K bytes [64q + 32h, +32) of its row in both operands
-      const int co = 64 * q + 32 * h;
-      v8i ah[TI], al[TI], bw[TJ];
+      const int co = 64 * q + 16 * h;
+      const v8i ah = lds_operand(cur + (wm + r) * kGRow + co);
+      const v8i al = lds_operand(cur + (BM + wm + r) * kGRow + co);
+      v8i bw[TJ];
 #pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        ah[i] = lds_v8(cur + (wm + 32 * i + r) * kGRow + co);
-        al[i] = lds_v8(cur + (BM + wm + 32 * i + r) * kGRow + co);
+      for (int j = 0; j < TJ; ++j) bw[j] = lds_operand(cur + (2 * BM + wn + 32 * j + r) * kGRow + co);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        t[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah, bw[j], t[j], 0, 0, 0,
+                                                               (int)(ws_hi >> (16 * q)), 0, 127);
+        t[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al, bw[j], t[j], 0, 0, 0,
+                                                               (int)(ws_lo >> (16 * q)), 0, 127);
       }
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) bw[j] = lds_v8(cur + (2 * BM + wn + 32 * j + r) * kGRow + co);
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          t[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ah[i], bw[j], t[i][j], 0, 0, 0, 127, 0, 127);
-          t[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(al[i], bw[j], t[i][j], 0, 0, 0, 127, 0, 127);
-        }
     }
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(t[i][j][e], swj[j], acc[i][j][e]);
+      for (int e = 0; e < 16; ++e) acc[j][e] = fmaf(t[j][e], swj[j], acc[j][e]);
   };
 
   // Prologue: blocks 0..D-1 in registers, block 0 in LDS stage 0, block D
   // loaded into the freed register set.
 #pragma unroll
-  for (int d = 0; d < D; ++d) gload(st[d], scv[d], d);
-  sstore(smem, st[0], scv[0]);
-  gload(st[0], scv[0], D);
+  for (int d = 0; d < D; ++d) gload(sa[d], sb[d], scv[d], d);
+  sstore(smem, sa[0], sb[0], scv[0]);
+  gload(sa[0], sb[0], scv[0], D);
   __syncthreads();
   // Invariant at step k: LDS stage (k % NST) holds block k, register set
   // (k + 1) % D holds block k + 1.
@@ -240,8 +254,8 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
       mma_block(smem + (NST == 2 ? (k & 1) * STAGE : 0));
       if constexpr (NST == 1) __syncthreads();   // one stage: every wave is done reading it
       const int nx = (d + 1) % D;   // static once the loop is unrolled
-      sstore(smem + (NST == 2 ? ((k + 1) & 1) * STAGE : 0), st[nx], scv[nx]);
-      gload(st[nx], scv[nx], k + 1 + D);
+      sstore(smem + (NST == 2 ? ((k + 1) & 1) * STAGE : 0), sa[nx], sb[nx], scv[nx]);
+      gload(sa[nx], sb[nx], scv[nx], k + 1 + D);
       __syncthreads();
     }
   }
@@ -252,38 +266,31 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint8_t* xhi, 
     float* pz = part + (size_t)blockIdx.z * M * ldp;
     const int ng0 = (int)blockIdx.x * BN;
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int e = 0; e < 16; ++e) {
+      const int m = mb + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m >= M) continue;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = mb + wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m >= M) continue;
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) pz[(size_t)m * ldp + ng0 + wn + 32 * j + r] = acc[i][j][e];
-      }
+      for (int j = 0; j < TJ; ++j) pz[(size_t)m * ldp + ng0 + wn + 32 * j + r] = acc[j][e];
+    }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < TI; ++i) {
+  for (int e = 0; e < 16; ++e) {
+    const int m = mb + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+    if (m >= M) continue;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = mb + wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m >= M) continue;
-      const float s = sx[m];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int n = nb + wn + 32 * j + r;
-        if (n < N) y[(size_t)m * N + n] = f2bf(acc[i][j][e] * s);
-      }
+    for (int j = 0; j < TJ; ++j) {
+      const int n = nb + wn + 32 * j + r;
+      if (n < N) y[(size_t)m * N + n] = f2bf(acc[j][e]);
     }
   }
 }
 
-// Split-K finish: y = bf16(sx[m] * sum_z part[z][m][column]), summed in z
-// order; columns past a segment's N (tile padding) are skipped.  Four
-// columns per thread (segments start at multiples of 64 columns).
+// Split-K finish: y = bf16(sum_z part[z][m][column]), summed in z order;
+// columns past a segment's N (tile padding) are skipped.  Four columns per
+// thread (segments start at multiples of 64 columns).
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
-                                                                 int ldp, const float* sx,
-                                                                 GemmGroup g, int bn) {
+                                                                 int ldp, GemmGroup g, int bn) {
   const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (q >= (size_t)M * ldp / 4) return;
   const int m = (int)(q / (ldp / 4)), ng = (int)(q % (ldp / 4)) * 4;
@@ -296,11 +303,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* pa
   if (n >= N) return;
   f32x4 acc = *(const f32x4*)(part + (size_t)m * ldp + ng);
   for (int z = 1; z < S; ++z) acc += *(const f32x4*)(part + ((size_t)z * M + m) * ldp + ng);
-  const float s = sx[m];
   uint16_t* y = g.y[si] + (size_t)m * N + n;
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    if (n + c < N) y[c] = f2bf(acc[c] * s);
+    if (n + c < N) y[c] = f2bf(acc[c]);
 }
 
 template <int BN>
@@ -320,62 +326,60 @@ GemmGroup make_group(const QhGemmSeg* seg, int nseg, int& tiles_n) {
   return g;
 }
 
-template <typename ScaleT, int BM, int BN, int NST, int D>
-void launch_gemm_lds(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
-                     int nseg, int M, int K, hipStream_t st, int S = 1, float* part = nullptr) {
+template <typename ScaleT, int BN, int NST, int D>
+void launch_gemm_lds(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K,
+                     hipStream_t st, int S = 1, float* part = nullptr) {
   int tiles_n = 0;
   const GemmGroup g = make_group<BN>(seg, nseg, tiles_n);
-  dim3 grid(tiles_n, (M + BM - 1) / BM, S);
+  dim3 grid(tiles_n, (M + kBM - 1) / kBM, S);
   const int ldp = tiles_n * BN;
-  hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BM, BN, NST, D>), grid, dim3(256),
-                     NST * (size_t)gemm_stage_bytes(BM, BN), st, xhi, xlo, sx, g, M, K,
-                     S > 1 ? part : nullptr, ldp);
+  hipLaunchKernelGGL((gemm_e4m3_lds_kernel<ScaleT, BN, NST, D>), grid, dim3(256),
+                     NST * (size_t)gemm_stage_bytes(BN), st, x, g, M, K, S > 1 ? part : nullptr,
+                     ldp);
   if (S > 1) {
     const size_t quads = (size_t)M * ldp / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256),
-                       0, st, (const float*)part, S, M, ldp, sx, g, BN);
+                       0, st, (const float*)part, S, M, ldp, g, BN);
   }
 }
 
-// 64x64 tiles.  With at least three tiles per CU, one LDS stage (27.6 KB)
-// lets four workgroups share a CU; with fewer tiles, two stages and two K
-// blocks in flight per workgroup.  M = 512: 9216 x 2560 50 us (1 stage) vs
-// 55 us (2 stages); 2560 x 9216 67 us (2 stages, 2 in flight) vs 70 us.
-// S > 1: split-K over S slices of K (partials in `part`); the variant is
-// chosen by the workgroup count tiles * S and the per-slice K block count.
+// 64x64 tiles.  With at least three tiles per CU, one LDS stage lets several
+// workgroups share a CU; with fewer tiles, two stages and two K blocks in
+// flight per workgroup.  S > 1: split-K over S slices of K (partials in
+// `part`); the variant is chosen by the workgroup count tiles * S and the
+// per-slice K block count.
 template <typename ScaleT>
-void launch_gemm_small(const uint8_t* xhi, const uint8_t* xlo, const float* sx, const QhGemmSeg* seg,
-                       int nseg, int M, int K, long tiles, hipStream_t st, int cus, int S,
-                       float* part) {
+void launch_gemm_small(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, long tiles,
+                       hipStream_t st, int cus, int S, float* part) {
   const int kbl = K / 128 / S;
   if (tiles * S >= 3L * cus)
-    launch_gemm_lds<ScaleT, 64, 64, 1, 1>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
+    launch_gemm_lds<ScaleT, 64, 1, 1>(x, seg, nseg, M, K, st, S, part);
   else if (kbl % 2 == 0)
-    launch_gemm_lds<ScaleT, 64, 64, 2, 2>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
+    launch_gemm_lds<ScaleT, 64, 2, 2>(x, seg, nseg, M, K, st, S, part);
   else
-    launch_gemm_lds<ScaleT, 64, 64, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st, S, part);
+    launch_gemm_lds<ScaleT, 64, 2, 1>(x, seg, nseg, M, K, st, S, part);
 }
-
-std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_bytes = 0;
 
 }  // namespace
 
-// Workspace: the activation's hi and lo E4M3 terms (M x K bytes each), the
-// row scales, then the split-K partials.  A split GEMM runs S * tiles <= 3 per
-// CU workgroups of 64x64 fp32 partials, so kSplitPartBytes covers up to 1024
-// of them (341 CUs).
+// Split-K partials: a split GEMM runs S * tiles <= 3 per CU workgroups of
+// 64x64 fp32 partials, so this covers up to 1024 of them (341 CUs).
 constexpr size_t kSplitPartBytes = (size_t)1024 * 64 * 64 * sizeof(float);
 
 size_t qh_gemm_workspace_bytes(int M, int K) {
-  return (size_t)M * K * 2 + (size_t)M * sizeof(float) + 512 + kSplitPartBytes;
+  (void)M;
+  (void)K;
+  return kSplitPartBytes;
 }
 
 int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* seg, int nseg,
                                  bool scale_bf16, void* ws, hipStream_t st) {
-  if (K % 128 != 0) {
-    qh_set_error("gemm: K=%d must be a multiple of 128", K);
+  if (K <= 0 || K % 128 != 0 || M <= 0) {
+    qh_set_error("gemm: M=%d, K=%d: need M > 0 and K a positive multiple of 128", M, K);
+    return -1;
+  }
+  if (!x || (uintptr_t)x % 16 != 0) {
+    qh_set_error("gemm: the activation must be a 16-byte aligned device pointer");
     return -1;
   }
   if (nseg < 1 || nseg > 4) {
@@ -391,40 +395,34 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
     tiles64 += (seg[t].N + 63) / 64;
     tiles128 += (seg[t].N + 127) / 128;
   }
-  uint8_t* xhi = (uint8_t*)ws;
-  uint8_t* xlo = xhi + (size_t)M * K;
-  float* sx = (float*)(((uintptr_t)(xlo + (size_t)M * K) + 255) & ~(uintptr_t)255);
-  hipLaunchKernelGGL(quant_rows_kernel, dim3(M), dim3(256), 0, st, (const uint16_t*)x, xhi, xlo,
-                     sx, K);
-  // 64x64 tiles unless 128x128 tiles give at least two per CU: at prefill
-  // sizes (M of a few hundred rows) the smaller tiles keep every CU busy and
-  // measured faster (M = 512: 63 vs 89 us for 9216 x 2560).
+  const uint16_t* xa = (const uint16_t*)x;
+  const long mt = (M + kBM - 1) / kBM;
   int cus = 256, dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  const bool small = tiles128 * ((M + 127) / 128) < 2L * cus;
-  if (small) {
-    const long tiles = tiles64 * ((M + 63) / 64);
-    // Split-K when there are no more tiles than CUs: the largest S <= 8
-    // dividing the K blocks with >= 4 blocks per slice and S * tiles <= 3 per
-    // CU, so each workgroup walks fewer serial K steps.  The extra reduce
-    // launch costs more than it saves above that (M = 128: 9216 x 2560, 288
-    // tiles, 24.7 us unsplit vs 28.8 us in 2; 2560 x 9216, 80 tiles, 46.5 vs
-    // 28.7 us in 8).
-    const int KB = K / 128;
-    int S = 1;
-    for (int c = 8; c >= 2 && tiles <= cus; --c)
-      if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
-          (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes) {
-        S = c;
-        break;
-      }
-    float* part = (float*)(((uintptr_t)(sx + M) + 255) & ~(uintptr_t)255);
-    if (scale_bf16) launch_gemm_small<uint16_t>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus, S, part);
-    else launch_gemm_small<float>(xhi, xlo, sx, seg, nseg, M, K, tiles, st, cus, S, part);
-  } else {
-    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
-    else launch_gemm_lds<float, 128, 128, 2, 1>(xhi, xlo, sx, seg, nseg, M, K, st);
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  // 64x128 tiles while they give at least two per CU (the A split is shared by
+  // twice the W rows); 64x64 below that, so every CU stays busy.
+  if (tiles128 * mt >= 2L * cus) {
+    if (scale_bf16) launch_gemm_lds<uint16_t, 128, 2, 1>(xa, seg, nseg, M, K, st);
+    else launch_gemm_lds<float, 128, 2, 1>(xa, seg, nseg, M, K, st);
+    return 0;
   }
+  const long tiles = tiles64 * mt;
+  // Split-K (caller workspace only) when there are no more tiles than CUs:
+  // the largest S <= 8 dividing the K blocks with >= 4 blocks per slice and
+  // S * tiles <= 3 per CU, so each workgroup walks fewer serial K steps.
+  const int KB = K / 128;
+  int S = 1;
+  for (int c = 8; ws && c >= 2 && tiles <= cus; --c)
+    if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
+        (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes) {
+      S = c;
+      break;
+    }
+  float* part = (float*)ws;
+  if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
+  else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   return 0;
 }
 
@@ -434,30 +432,9 @@ int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y,
   return qh_launch_gemm_e4m3_group_ws(x, M, K, &seg, 1, scale_bf16, ws, st);
 }
 
-// Without a caller workspace, the library keeps one internal buffer that grows
-// on demand (hipMalloc outside any captured region; the reference ABI passes
-// no workspace).
+// Without a caller workspace (the reference ABI passes none): no split-K and
+// nothing allocated.
 int qh_launch_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
                         int kb, bool scale_bf16, hipStream_t st) {
-  const size_t need = qh_gemm_workspace_bytes(M, K);
-  void* ws = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (g_ws_bytes < need) {
-      if (g_ws) {
-        (void)hipStreamSynchronize(st);
-        (void)hipFree(g_ws);
-        g_ws = nullptr;
-        g_ws_bytes = 0;
-      }
-      if (hipMalloc(&g_ws, need) != hipSuccess) {
-        g_ws = nullptr;
-        qh_set_error("gemm: workspace allocation of %zu bytes failed", need);
-        return -1;
-      }
-      g_ws_bytes = need;
-    }
-    ws = g_ws;
-  }
-  return qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scale_bf16, ws, st);
+  return qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scale_bf16, nullptr, st);
 }

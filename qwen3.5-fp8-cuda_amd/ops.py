@@ -38,7 +38,9 @@ def _check_linear(x2d, w_bytes, w_scale):
 
 
 def fp8_linear(input_bf16, w_bytes, w_scale_inv, out=None):
-    """FP8 linear y = x W^T (main.py:242-270)."""
+    """FP8 linear y = x W^T (main.py:242-270).  bf16 scales go to the
+    reference symbols (launch_gemv_v4_extern for M == 1, fp8_gemm_batch for
+    M > 1), fp32 scales to the native entry points."""
     lib = abi.load()
     orig = input_bf16.shape
     K = orig[-1]
@@ -65,10 +67,16 @@ def fp8_linear(input_bf16, w_bytes, w_scale_inv, out=None):
                                        abi.ptr(w_bytes), abi.ptr(w_scale_inv), abi.ptr(y), N, kb,
                                        None, None, None, 0, 0, None, None, None, 0, 0,
                                        None, None, None, 0, 0, 0, st), "fp8_linear")
+    elif bf16_scales:
+        lib.qh_clear_error()
+        lib.fp8_gemm_batch(abi.ptr(x2d), abi.ptr(w_bytes), abi.ptr(w_scale_inv), abi.ptr(y),
+                           M, N, K, kb, st)
+        err = abi.last_error(lib)
+        if err:
+            raise abi.QhError(err)
     else:
         abi.check(lib.qh_gemm_e4m3(abi.ptr(x2d), abi.ptr(w_bytes), abi.ptr(w_scale_inv),
-                                   abi.ptr(y), M, N, K, kb, int(bf16_scales), None, st),
-                  "fp8_linear")
+                                   abi.ptr(y), M, N, K, kb, 0, None, st), "fp8_linear")
     return y.reshape(*orig[:-1], N)
 
 

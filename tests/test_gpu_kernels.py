@@ -245,7 +245,11 @@ def _attn_case(g, ctx, Hq=16, Hkv=4, D=256, rot=64, max_seq=None):
     return kc, vc, q_all, k_new, v_new, qn, kn
 
 
-@pytest.mark.parametrize("ctx,splits", [(1, 1), (17, 1), (130, 4), (4096, 32), (427, 32)])
+# (4096, 64), (2049, 64), (300, 64): the engine's split count for a 4096-slot
+# cache (engine.default_attn_splits), where the merge's lanes 32-63 carry
+# (m, l) pairs and the partials arrive in eight batches.
+@pytest.mark.parametrize("ctx,splits", [(1, 1), (17, 1), (130, 4), (4096, 32), (427, 32),
+                                        (4096, 64), (2049, 64), (300, 64)])
 def test_attn_decode(ctx, splits):
     """BASELINE config 4b (ctx 4096): q/k norm, partial RoPE (theta 1e7, 64 of
     256 dims), KV write at slot ctx-1, GQA 16/4, sigmoid gate."""
@@ -543,7 +547,7 @@ def test_gemm_e4m3(M, N, K):
     c = cos_sim(y.cpu().float(), ref)
     assert c >= 0.99999, f"gemm cosine {c}"
     assert_close(y, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="gemm")
-    y16 = ops.fp8_linear(cu(x), cu(w), cu(s.to(torch.bfloat16)))   # reference symbol fp8_gemm_batch
+    y16 = ops.fp8_linear(cu(x), cu(w), cu(s.to(torch.bfloat16)))   # bf16 scales: fp8_gemm_batch
     sync()
     ref16 = x.float() @ orc.dequant(w, s.to(torch.bfloat16).float()).t()
     assert cos_sim(y16.cpu().float(), ref16) >= 0.99999
@@ -576,3 +580,124 @@ def test_gemm_grouped_matches_single_launches(M):
         assert_close(a, b, rtol=2 ** -7, atol_frac=1e-6, what=f"grouped vs single, {n} rows")
         ref = x.float() @ orc.dequant(w, s).t()
         assert cos_sim(a.cpu().float(), ref) >= 0.99999
+
+
+# ------------------------------------------------- reference ABI, called directly
+def _ref_kb(w, s):
+    """main.py:249-251: the K_blocks code main.py passes for a scale tensor."""
+    k_blocks = s.shape[1]
+    return -k_blocks if s.shape[0] == w.shape[0] and k_blocks > 1 else k_blocks
+
+
+@pytest.mark.parametrize("M,N,K,mode", [(40, 2560, 2560, "block"), (7, 1000, 384, "block"),
+                                        (33, 256, 1024, "row"), (19, 384, 512, "row_block")])
+def test_fp8_gemm_batch_reference_abi(M, N, K, mode):
+    """fp8_gemm_batch exactly as main.py:262-269 calls it: bf16 scale_inv, the
+    K_blocks code of main.py:249-251, the null stream, no workspace."""
+    import ctypes
+    g = gen(M * 7 + N + K)
+    W = randn(g, N, K, std=0.02)
+    if mode == "block":
+        w, s = orc.quantize_block_fp8(W)
+    elif mode == "row":
+        s = (W.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12)
+        w = (W / s).to(torch.float8_e4m3fn).view(torch.uint8)
+    else:
+        s = (W.view(N, K // 128, 128).abs().amax(dim=2) / 448.0).clamp(min=1e-12)
+        w = (W.view(N, K // 128, 128) / s.unsqueeze(-1)).to(torch.float8_e4m3fn).view(
+            torch.uint8).reshape(N, K)
+    s16 = s.to(torch.bfloat16)
+    x = bf(randn(g, M, K))
+    ref = x.float() @ orc.dequant(w, s16.float()).t()
+    lib = abi.load()
+    dx, dw, ds = cu(x), cu(w.contiguous()), cu(s16.contiguous())
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    lib.qh_clear_error()
+    lib.fp8_gemm_batch(abi.ptr(dx), abi.ptr(dw), abi.ptr(ds), abi.ptr(y), M, N, K,
+                       _ref_kb(w, s16), ctypes.c_void_p(0))
+    sync()
+    assert abi.last_error() == ""
+    c = cos_sim(y.cpu().float(), ref)
+    assert c >= 0.99999, f"fp8_gemm_batch cosine {c}"
+    assert_close(y, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="fp8_gemm_batch")
+
+
+@pytest.mark.parametrize("path", ["fp8_gemm_batch", "qh_gemm_e4m3_ws"])
+def test_gemm_activation_outlier_channels(path):
+    """Channels 100-3000x larger than the rest sit in the same 32-element runs
+    as ordinary values.  Their weight columns are zero, so the output is the
+    ordinary channels' product alone: any precision the outliers cost their
+    neighbours in the activation split shows up in full."""
+    M, N, K = 64, 512, 1024
+    g = gen(77)
+    w, s = quant(g, N, K)
+    cols = torch.tensor([3, 77, 500, 901, 902])
+    w = w.clone()
+    w[:, cols] = 0                                  # E4M3 +0
+    x = randn(g, M, K)
+    x[:, cols] = torch.tensor([1000.0, -300.0, 100.0, 3000.0, -1500.0])
+    x[::3, 40] = 2000.0                             # row-dependent outliers too
+    w[:, 40] = 0
+    x = bf(x)
+    ref = x.float() @ orc.dequant(w, s).t()
+    lib = abi.load()
+    dx, dw = cu(x), cu(w)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    if path == "fp8_gemm_batch":
+        s16 = s.to(torch.bfloat16)
+        ref = x.float() @ orc.dequant(w, s16.float()).t()
+        lib.fp8_gemm_batch(abi.ptr(dx), abi.ptr(dw), abi.ptr(cu(s16)), abi.ptr(y), M, N, K, K // 128,
+                           abi.stream_handle())
+    else:
+        ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
+        abi.check(lib.qh_gemm_e4m3(abi.ptr(dx), abi.ptr(dw), abi.ptr(cu(s)), abi.ptr(y), M, N, K,
+                                   K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm")
+    sync()
+    assert abi.last_error() == ""
+    c = cos_sim(y.cpu().float(), ref)
+    assert c >= 0.99999, f"{path}: cosine {c} with outlier channels"
+    assert_close(y, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what=path)
+
+
+def test_launch_fused_qkv_reference_abi():
+    """launch_fused_qkv with main.py:281-298's arguments: bf16 scale_inv, K_blk =
+    s_q.shape[1] and the N_*_blk row-block counts."""
+    g = gen(31)
+    K, Nq, Nkv = 2560, 8192, 1024
+    x = bf(randn(g, K))
+    mats = [quant(g, n, K) for n in (Nq, Nkv, Nkv)]
+    mats = [(w, s.to(torch.bfloat16)) for w, s in mats]
+    refs = [orc.linear(x.float(), orc.dequant(w, s.float())) for w, s in mats]
+    lib = abi.load()
+    outs = [torch.empty(w.shape[0], dtype=torch.bfloat16, device=DEV) for w, _ in mats]
+    (wq, sq), (wk, sk), (wv, sv) = [(cu(w), cu(s)) for w, s in mats]
+    lib.qh_clear_error()
+    lib.launch_fused_qkv(abi.ptr(cu(x)), abi.ptr(wq), abi.ptr(wk), abi.ptr(wv), abi.ptr(sq),
+                         abi.ptr(sk), abi.ptr(sv), *[abi.ptr(o) for o in outs], K, Nq, Nkv, Nkv,
+                         sq.shape[1], sq.shape[0], sk.shape[0], sv.shape[0], abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    for o, r, name in zip(outs, refs, "qkv"):
+        assert_close(o, r, what=f"launch_fused_qkv {name}")
+
+
+@pytest.mark.parametrize("D,seq", [(256, 999), (128, 300)])
+def test_launch_fused_attn_reference_abi(D, seq):
+    """launch_fused_attn (fused_kernels.cu:1027-1043): attention of already
+    normalised, rotated query heads over the cache, no cache write."""
+    g = gen(D + seq)
+    Hq, Hkv, max_seq = 16, 4, 1024
+    kc = bf(randn(g, Hkv, max_seq, D)).float()
+    vc = bf(randn(g, Hkv, max_seq, D)).float()
+    q = bf(randn(g, Hq * D))
+    ref = orc.attn_only(q.float(), kc, vc, seq, Hq, Hkv)
+    lib = abi.load()
+    kcg, vcg = cu(bf(kc)), cu(bf(vc))
+    out = torch.empty(Hq * D, dtype=torch.bfloat16, device=DEV)
+    lib.qh_clear_error()
+    lib.launch_fused_attn(abi.ptr(cu(q)), abi.ptr(kcg), abi.ptr(vcg), abi.ptr(out), seq, max_seq, D,
+                          Hq, Hkv, abi.stream_handle())
+    sync()
+    assert abi.last_error() == ""
+    assert_close(out, ref, atol_frac=1e-3, what=f"launch_fused_attn D={D}")
+    assert torch.equal(kcg.cpu().float(), kc), "launch_fused_attn must not write the cache"
