@@ -212,7 +212,8 @@ size_t qh_sample_workspace_size(int V);
  * sampling of one bf16 logits row entirely on the device.  temperature > 0
  * scales the logits; rep_penalty > 1 penalises the distinct ids of the window
  * hist[max(lo, p - window) .. p), p = *pos_dev + pos_offset (pos when pos_dev
- * is null), lo = *lo_dev (0 when null), window <= 64; top-min(2000, V)
+ * is null), lo = *lo_dev (0 when null), window <= 64, slots clipped to
+ * [0, hist_len) (hist_len > 0 when hist is given); top-min(2000, V)
  * candidates normalised against the full vocabulary, full-softmax fallback
  * when their mass is below top_p, top-p cut, one draw (SplitMix64 of seed and
  * *counter, which advances by one).  Writes *tok_out, hist[p] when hist is
@@ -224,7 +225,8 @@ size_t qh_sample_workspace_size(int V);
  * arrival counters reset themselves); calls sharing one workspace must not
  * overlap. */
 int qh_sample_top_p(const void* logits, int V, float temperature, float top_p, float rep_penalty,
-                    int64_t* hist, const int* pos_dev, int pos, int pos_offset, const int* lo_dev,
+                    int64_t* hist, int hist_len, const int* pos_dev, int pos, int pos_offset,
+                    const int* lo_dev,
                     int window, uint64_t seed, uint64_t* counter, void* ws, int64_t* tok_out,
                     const void* embed, void* h, int D, int64_t* info, qh_stream_t stream);
 
@@ -263,10 +265,9 @@ int qh_gemv_e4m3_gated(const void* core, const void* z, const void* norm_w, int 
                        const void* res, const void* w, const void* s, void* y, int n, int kb,
                        int scales_bf16, qh_stream_t stream);
 
-/* Workspace bytes for qh_gemm_e4m3 / qh_gemm_e4m3_grouped with M rows of K:
- * the activation's hi and lo E4M3 terms (2 M K bytes), the row scales and a
- * fixed 16 MiB region for split-K partials.  Calls sharing a workspace must
- * not overlap. */
+/* Workspace bytes for qh_gemm_e4m3 / qh_gemm_e4m3_grouped (a fixed 16 MiB of
+ * split-K partials, whatever M and K).  The workspace is optional: without one
+ * the GEMM does not split K.  Calls sharing a workspace must not overlap. */
 size_t qh_gemm_workspace_size(int M, int K);
 
 /* Prefill GEMM on the fp8 matrix cores (fp8_gemm_batch semantics). */
@@ -276,8 +277,7 @@ int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, in
 /* Grouped prefill GEMM; no counterpart in the reference, which runs each
  * projection as its own fp8_gemm_batch (main.py:262-269).  Up to 4 projections
  * of one activation x [M, K] (segment t: y_t [M, n_t] = bf16(x . deq(w_t)^T),
- * scale mode kb_t), one activation split and one launch; ws as for
- * qh_gemm_e4m3 (qh_gemm_workspace_size(M, K) bytes, required). */
+ * scale mode kb_t) in one launch; ws as for qh_gemm_e4m3 (optional). */
 int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0, const void* s0,
                          void* y0, int n0, int kb0, const void* w1, const void* s1, void* y1,
                          int n1, int kb1, const void* w2, const void* s2, void* y2, int n2,

@@ -451,7 +451,9 @@ class OracleModel:
         gated = gated_rmsnorm(core, z.view(Hv, dv), ly["norm_w"], 1e-6, bf16_steps=True)
         return linear(gated.reshape(-1), ly["out_proj"])
 
-    def decode_token(self, tok, pos):
+    def decode_token(self, tok, pos, trace=None):
+        """One decode step (main.py:1509-1547); with a list `trace`, the hidden
+        state after every layer is appended to it."""
         cfg = self.cfg
         h = self.embed[tok].clone()
         for i in range(cfg.num_hidden_layers):
@@ -460,6 +462,8 @@ class OracleModel:
             o = self._full_decode(i, hn, pos) if cfg.is_full(i) else self._gdn_decode(i, hn)
             h, _ = mlp_decode(h, o, ly["post_attention_layernorm"], ly["gate_proj"],
                               ly["up_proj"], ly["down_proj"], self.eps)
+            if trace is not None:
+                trace.append(h.clone())
         logits, tok = lm_head_argmax(h, self.norm_f, self.lm_head, self.eps)
         return logits, tok
 
@@ -489,7 +493,7 @@ class OracleModel:
         out = bf16(out.reshape(s, Hq * D) * bf16(torch.sigmoid(gate)))
         return linear(out, ly["o_proj"])
 
-    def _gdn_prefill(self, i, hn):
+    def _gdn_prefill(self, i, hn, past=0):
         cfg, ly = self.cfg, self.layers[i]
         s = hn.shape[0]
         mixed = linear(hn, ly["in_proj_qkv"])
@@ -510,34 +514,53 @@ class OracleModel:
         v = y[:, 2 * kd:].reshape(s, Hv, dv)
         g, beta = linear_gates(a, b, ly["A_log"], ly["dt_bias"])
         S = self.rec_state[i]
-        S.zero_()
+        if past == 0:
+            S.zero_()   # initial_state=None at past_len == 0 (main.py:1130-1131)
         o = gated_delta_rule_seq(q * (1.0 / math.sqrt(dk)), k, v, g, beta, S)
         gated = gated_rmsnorm(bf16(o), z.view(s, Hv, dv), ly["norm_w"], 1e-6, bf16_steps=True)
         return linear(gated.reshape(s, -1), ly["out_proj"])
 
-    def prefill(self, ids, past=0):
+    def prefill(self, ids, past=0, keep=1, trace=None):
+        """Batch prefill of tokens at positions past .. past + s - 1
+        (main.py:1550-1566); logits [keep, V] of the last `keep` positions and
+        the greedy token after the last one.  With a list `trace`, the last
+        token's hidden state after every layer is appended to it."""
         cfg = self.cfg
         h = self.embed[ids]
         for i in range(cfg.num_hidden_layers):
             ly = self.layers[i]
             hn = rmsnorm(h, ly["input_layernorm"], self.eps)
-            o = self._full_prefill(i, hn, past) if cfg.is_full(i) else self._gdn_prefill(i, hn)
+            o = (self._full_prefill(i, hn, past) if cfg.is_full(i)
+                 else self._gdn_prefill(i, hn, past))
             h = bf16(h + o)
             hn = rmsnorm(h, ly["post_attention_layernorm"], self.eps)
             h = bf16(h + mlp_prefill(hn, ly["gate_proj"], ly["up_proj"], ly["down_proj"]))
-        return lm_head_argmax(h[-1], self.norm_f, self.lm_head, self.eps)
+            if trace is not None:
+                trace.append(h[-1].clone())
+        rows = [lm_head_argmax(r, self.norm_f, self.lm_head, self.eps) for r in h[-keep:]]
+        return torch.stack([r[0].reshape(-1) for r in rows]), rows[-1][1]
 
     # ---- API ----------------------------------------------------------------
-    def forward(self, input_ids, past_len=0):
+    def forward(self, input_ids, past_len=0, logits_to_keep=1):
+        """Logits [k, V] of the last k = min(logits_to_keep, s) positions (all s
+        for 0), main.py:1569-1604.  past_len == 0 starts a new sequence with
+        cleared caches, as the reference's callers do (main.py:1617, 1711)."""
         ids = [int(t) for t in torch.as_tensor(input_ids).reshape(-1)]
-        if len(ids) == 1 or self.prefill_mode == "sequential":
+        s = len(ids)
+        if logits_to_keep < 0:
+            raise ValueError("logits_to_keep must be non-negative")
+        keep = s if logits_to_keep == 0 else min(logits_to_keep, s)
+        if past_len == 0:
+            self._reset_cache()
+        if s == 1 or self.prefill_mode == "sequential":
+            rows = []
             for j, t in enumerate(ids):
                 logits, _ = self.decode_token(t, past_len + j)
-        else:
-            if past_len != 0:
-                raise ValueError("oracle prefill supports past_len == 0 only")
-            logits, _ = self.prefill(torch.tensor(ids))
-        return logits.view(1, -1)
+                if j >= s - keep:
+                    rows.append(logits.reshape(-1))
+            return torch.stack(rows)
+        logits, _ = self.prefill(torch.tensor(ids), past_len, keep)
+        return logits
 
     def greedy(self, prompt, n_steps):
         """Prompt, then n greedy steps; returns the n generated tokens and the

@@ -74,8 +74,8 @@ NATIVE_SIGNATURES = {
     "qh_lm_head_argmax": (_i, [_vp, _vp, _f, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i,
                                _vp, _vp, _vp, _vp]),
     "qh_sample_workspace_size": (_sz, [_i]),
-    "qh_sample_top_p": (_i, [_vp, _i, _f, _f, _f, _vp, _vp, _i, _i, _vp, _i, _u64, _vp, _vp, _vp,
-                             _vp, _vp, _i, _vp, _vp]),
+    "qh_sample_top_p": (_i, [_vp, _i, _f, _f, _f, _vp, _i, _vp, _i, _i, _vp, _i, _u64, _vp, _vp,
+                             _vp, _vp, _vp, _i, _vp, _vp]),
     "qh_embed": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "qh_add_bf16": (_i, [_vp, _vp, _vp, _i, _vp]),
     "qh_linear_gates": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),

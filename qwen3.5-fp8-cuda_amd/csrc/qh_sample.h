@@ -18,8 +18,10 @@ struct QhSampleParams {
   // Recent window (main.py:1720-1731 keeps the last 50 generated tokens): the
   // new token goes to slot p = *pos_dev + pos_offset (or `pos` without
   // pos_dev); the window is hist[max(lo, p - window) .. p) with lo = *lo_dev
-  // (or 0 without lo_dev).
+  // (or 0 without lo_dev).  Only slots in [0, hist_len) are read or written:
+  // a slot past the end gets no write-back and the window is clipped to it.
   int64_t* hist;            // token history (optional: no penalty, no write-back)
+  int hist_len;             // entries in hist
   const int* pos_dev;
   int pos;
   int pos_offset;

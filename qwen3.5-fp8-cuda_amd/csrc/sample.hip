@@ -114,7 +114,8 @@ __device__ __forceinline__ Window window_of(const QhSampleParams& p) {
   w.slot = (p.pos_dev ? *p.pos_dev : p.pos) + p.pos_offset;
   const int lo0 = p.lo_dev ? *p.lo_dev : 0;
   w.lo = max(max(lo0, 0), w.slot - p.window);
-  w.n = (p.hist && p.window > 0) ? max(0, min(w.slot - w.lo, p.window)) : 0;
+  const int end = min(w.slot, p.hist_len);  // window slots stay inside hist
+  w.n = (p.hist && p.window > 0) ? max(0, min(end - w.lo, p.window)) : 0;
   return w;
 }
 
@@ -505,7 +506,7 @@ __global__ __launch_bounds__(256) void sample_locate_kernel(QhSampleParams p, Sa
   if (tid == 0) {
     *p.tok_out = tok;
     const int slot = (int)w.sel[3];
-    if (p.hist && slot >= 0) p.hist[slot] = tok;
+    if (p.hist && slot >= 0 && slot < p.hist_len) p.hist[slot] = tok;
     if (p.info) p.info[12] = s_tok;
   }
   if (p.embed && p.h) {
@@ -529,6 +530,10 @@ int qh_launch_sample(const QhSampleParams& p, hipStream_t st) {
   }
   if (!(p.top_p > 0.0f) || !(p.rep_penalty > 0.0f)) {
     qh_set_error("sample: top_p=%g and rep_penalty=%g must be positive", p.top_p, p.rep_penalty);
+    return -1;
+  }
+  if (p.hist && p.hist_len <= 0) {
+    qh_set_error("sample: a token history needs hist_len > 0");
     return -1;
   }
   if (p.embed && (!p.h || p.D <= 0)) {

@@ -82,6 +82,7 @@ class Qwen35FP8Engine:
         self.tok = torch.zeros(1, 1, dtype=torch.int64, device=dev)
         self.tok_hist = torch.zeros(max_seq_len, dtype=torch.int64, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self._host_pos = 0       # host mirror of pos (bounds the steps the host enqueues)
         self.lm_scratch = torch.zeros(int(self.lib.qh_lm_head_scratch_bytes(V)), dtype=torch.uint8,
                                       device=dev)
         self.lm_counter = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -148,6 +149,7 @@ class Qwen35FP8Engine:
             if s is not None:
                 s.zero_()
         self.pos.zero_()
+        self._host_pos = 0
         self.sample_ctr.zero_()
 
     # ------------------------------------------------------------- launches
@@ -316,7 +318,8 @@ class Qwen35FP8Engine:
         cfg = self.cfg
         abi.check(self.lib.qh_sample_top_p(
             abi.ptr(self.logits), cfg.vocab_size, sp["temperature"], sp["top_p"], sp["rep_penalty"],
-            abi.ptr(self.tok_hist), abi.ptr(self.pos), 0, -1, abi.ptr(self.gen_lo), sp["window"],
+            abi.ptr(self.tok_hist), self.max_seq_len, abi.ptr(self.pos), 0, -1,
+            abi.ptr(self.gen_lo), sp["window"],
             sp["seed"], abi.ptr(self.sample_ctr), abi.ptr(self.sample_ws), abi.ptr(self.tok),
             abi.ptr(self.w.embed), abi.ptr(self.h), cfg.hidden_size, abi.ptr(self.sample_info),
             abi.stream_handle()), "sample_top_p")
@@ -361,8 +364,18 @@ class Qwen35FP8Engine:
         self.graph = g
         return g
 
+    def _advance(self, n):
+        """Host-side mirror of the device position: a decode step consumes the
+        token at position pos (KV slot and history entry pos) and leaves
+        pos + 1, so n more steps need pos + n <= max_seq_len."""
+        if self._host_pos + n > self.max_seq_len:
+            raise ValueError(f"{n} decode step(s) from position {self._host_pos} exceed "
+                             f"max_seq_len={self.max_seq_len}")
+        self._host_pos += n
+
     def step(self):
         """One greedy decode step from the device-resident token/position."""
+        self._advance(1)
         if self.graph is not None:
             self.graph.replay()
         else:
@@ -371,28 +384,46 @@ class Qwen35FP8Engine:
     # ------------------------------------------------------ reference API
     @torch.inference_mode()
     def forward(self, input_ids, past_len=0, logits_to_keep=1):
-        """bf16 logits [1, vocab] of the last input position (main.py:1569-1604)."""
+        """bf16 logits [k, vocab] of the last k = min(logits_to_keep, s) input
+        positions, all s for logits_to_keep=0 (main.py:1569-1604).
+
+        past_len == 0 starts a new sequence: the recurrent state, conv ring and
+        position are cleared first (the reference ignores the stored recurrent
+        state there, main.py:1130-1131, and its callers reset the caches before
+        every prompt, main.py:1617/1711).  s > 1 runs the batch prefill at any
+        past_len (main.py:1550-1566); s == 1 is one decode step."""
         if isinstance(input_ids, list):
             input_ids = torch.tensor([input_ids], dtype=torch.long, device=self.device)
         ids = input_ids.reshape(-1).to(self.device, torch.int64)
         s = ids.numel()
+        if s < 1:
+            raise ValueError("forward needs at least one input id")
         if past_len < 0 or past_len + s > self.max_seq_len:
             raise ValueError(f"Sequence range [{past_len}, {past_len + s}) exceeds "
                              f"max_seq_len={self.max_seq_len}")
-        if logits_to_keep != 1:
-            raise ValueError("only logits_to_keep=1 is supported")
+        if logits_to_keep < 0:
+            raise ValueError("logits_to_keep must be non-negative")
+        keep = s if logits_to_keep == 0 else min(logits_to_keep, s)
+        if past_len == 0:
+            self._reset_cache()
         # the sampler's repetition window starts at the first generated token
         self.gen_lo.fill_(past_len + s - 1)
-        if s > 1 and past_len == 0 and self.batch_prefill:
-            return self.prefill_batch(ids)
+        if s > 1 and self.batch_prefill:
+            return self.prefill_batch(ids, past_len, keep)
         st = abi.stream_handle()
+        out = None
+        if keep > 1:
+            out = torch.empty(keep, self.cfg.vocab_size, dtype=torch.bfloat16, device=self.device)
         self.pos.fill_(past_len)
+        self._host_pos = past_len
         for t in range(s):
             abi.check(self.lib.qh_embed(abi.ptr(self.w.embed), abi.ptr(ids[t:t + 1]),
                                         abi.ptr(self.h), 1, self.cfg.hidden_size,
                                         self.cfg.vocab_size, st), "embed")
             self.step()
-        return self.logits.view(1, -1)
+            if out is not None and t >= s - keep:
+                out[t - (s - keep)].copy_(self.logits)
+        return out if out is not None else self.logits.view(1, -1)
 
     def prefill(self, ids):
         """Run the prompt; afterwards tok holds the greedy next token, h its
@@ -451,21 +482,28 @@ class Qwen35FP8Engine:
                                                 int(s0.dtype == torch.bfloat16), abi.ptr(ws),
                                                 abi.stream_handle()), "gemm_grouped")
 
-    def prefill_batch(self, ids):
-        """The reference's s > 1 prefill (main.py:1550-1566) for a prompt at
-        position 0: every projection as an FP8 GEMM over the M tokens, batch
-        attention / GatedDeltaNet kernels, then the lm_head + greedy argmax of
-        the last token.  Afterwards tok holds the next token, h its embedding
-        and pos = M (the recurrent state continues from the prompt)."""
+    def prefill_batch(self, ids, past=0, keep=1, trace=None):
+        """The reference's s > 1 prefill (main.py:1550-1566) of M tokens at
+        positions past .. past + M - 1: every projection as an FP8 GEMM over
+        the M tokens, batch attention / GatedDeltaNet kernels continuing from
+        the stored KV cache, conv ring and recurrent state (cleared first when
+        past == 0), then the lm_head + greedy argmax of the last token.
+        Afterwards tok holds the next token, h its embedding and pos = past + M.
+        Returns the bf16 logits of the last `keep` tokens [keep, vocab].
+        With a list `trace`, the last token's hidden state after each layer is
+        appended to it (a host copy per layer: diagnostics only)."""
         cfg, L = self.cfg, self.lib
         ids = ids.reshape(-1).to(self.device, torch.int64)
         M = ids.numel()
-        if M < 1 or M > self.max_seq_len:
-            raise ValueError(f"prompt of {M} tokens does not fit max_seq_len={self.max_seq_len}")
+        if M < 1 or past < 0 or past + M > self.max_seq_len:
+            raise ValueError(f"tokens [{past}, {past + M}) do not fit max_seq_len={self.max_seq_len}")
+        if not 1 <= keep <= M:
+            raise ValueError(f"keep={keep} outside [1, {M}]")
         B = self._prefill_buffers(M)
         st = abi.stream_handle()
         H, I, eps = cfg.hidden_size, cfg.intermediate_size, self.eps
-        self._reset_cache()
+        if past == 0:
+            self._reset_cache()
         h, hn, o, ws = B["h"][:M], B["hn"][:M], B["o"][:M], B["ws"]
         B["ids"][:M].copy_(ids)
         abi.check(L.qh_embed(abi.ptr(self.w.embed), abi.ptr(B["ids"]), abi.ptr(h), M, H,
@@ -483,12 +521,12 @@ class Qwen35FP8Engine:
                                          abi.ptr(ly["q_norm"]), abi.ptr(ly["k_norm"]),
                                          abi.ptr(self.rope_cos), abi.ptr(self.rope_sin),
                                          abi.ptr(B["q32"]), abi.ptr(self.k_cache[i]),
-                                         abi.ptr(self.v_cache[i]), M, Hq, Hkv, D, cfg.rotary_dim, 0,
-                                         self.max_seq_len, eps, st), "attn_prep")
+                                         abi.ptr(self.v_cache[i]), M, Hq, Hkv, D, cfg.rotary_dim,
+                                         past, self.max_seq_len, eps, st), "attn_prep")
                 abi.check(L.qh_attn_prefill(abi.ptr(B["q32"]), abi.ptr(q_all[:, D:]), Hq * 2 * D,
                                             2 * D, abi.ptr(self.k_cache[i]),
                                             abi.ptr(self.v_cache[i]), abi.ptr(B["att"]), M, Hq, Hkv,
-                                            D, 0, self.max_seq_len, st), "attn_prefill")
+                                            D, past, self.max_seq_len, st), "attn_prefill")
                 self._gemm(B["att"][:M], ly["o_proj"], o, M, ws)
             else:
                 Hk, Hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
@@ -500,8 +538,8 @@ class Qwen35FP8Engine:
                                         abi.ptr(ly["conv1d_w"]), abi.ptr(B["a"]), abi.ptr(B["b"]),
                                         abi.ptr(ly["A_log"]), abi.ptr(ly["dt_bias"]),
                                         abi.ptr(B["y"]), abi.ptr(B["qn"]), abi.ptr(B["kn"]),
-                                        abi.ptr(B["g"]), abi.ptr(B["beta"]), M, Hk, Hv, dk, dv, 0,
-                                        st), "gdn_prep")
+                                        abi.ptr(B["g"]), abi.ptr(B["beta"]), M, Hk, Hv, dk, dv,
+                                        past, st), "gdn_prep")
                 abi.check(L.qh_gdn_scan(abi.ptr(B["qn"]), abi.ptr(B["kn"]), abi.ptr(B["y"]),
                                         abi.ptr(B["g"]), abi.ptr(B["beta"]), abi.ptr(B["z"]),
                                         abi.ptr(ly["norm_w"]), abi.ptr(self.state[i]),
@@ -517,18 +555,69 @@ class Qwen35FP8Engine:
                                     st), "silu_mul")
             self._gemm(B["m"][:M], ly["down_proj"], o, M, ws)
             abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
-        self.pos.fill_(M - 1)
+            if trace is not None:
+                trace.append(h[M - 1].float().cpu())
+        out = None
+        if keep > 1:
+            # every kept position but the last: logits only (no token, position
+            # or history side effects)
+            out = torch.empty(keep, cfg.vocab_size, dtype=torch.bfloat16, device=self.device)
+            for j in range(keep - 1):
+                r = M - keep + j
+                abi.check(L.qh_lm_head_argmax(
+                    abi.ptr(h[r]), abi.ptr(self.w.norm_f), eps, H, abi.ptr(self.w.lm_head),
+                    cfg.vocab_size, abi.ptr(out[j]), abi.ptr(self.lm_scratch),
+                    abi.ptr(self.lm_counter), abi.ptr(self.tok), None, 0, None, None, None, st),
+                    "lm_head_argmax")
+        self.pos.fill_(past + M - 1)
+        self._host_pos = past + M
         abi.check(L.qh_lm_head_argmax(
             abi.ptr(h[M - 1]), abi.ptr(self.w.norm_f), eps, H, abi.ptr(self.w.lm_head),
             cfg.vocab_size, abi.ptr(self.logits), abi.ptr(self.lm_scratch),
             abi.ptr(self.lm_counter), abi.ptr(self.tok), abi.ptr(self.tok_hist), self.max_seq_len,
             abi.ptr(self.pos), abi.ptr(self.w.embed), abi.ptr(self.h), st), "lm_head_argmax")
         self._sample()
+        if out is not None:
+            out[keep - 1].copy_(self.logits)
+            return out
         return self.logits.view(1, -1)
+
+    @torch.inference_mode()
+    def decode_trace(self, tok, pos):
+        """One eager decode step of token `tok` at position `pos` that also
+        returns the hidden state after every layer (host copies; diagnostics
+        for per-layer parity against the oracle).  Leaves the engine as
+        forward([tok], pos) does; returns (per-layer hidden states, logits)."""
+        if pos < 0 or pos >= self.max_seq_len:
+            raise ValueError(f"position {pos} outside [0, {self.max_seq_len})")
+        if pos == 0:
+            self._reset_cache()
+        ids = torch.tensor([tok], dtype=torch.int64, device=self.device)
+        st = abi.stream_handle()
+        abi.check(self.lib.qh_embed(abi.ptr(self.w.embed), abi.ptr(ids), abi.ptr(self.h), 1,
+                                    self.cfg.hidden_size, self.cfg.vocab_size, st), "embed")
+        self.pos.fill_(pos)
+        self._host_pos = pos
+        self._advance(1)
+        n = self.cfg.num_hidden_layers
+        hs = []
+        self._pre(0)
+        for i in range(n):
+            self._mixer(i)
+            self._post(i)
+            hs.append(self.h.float().cpu())
+            if i + 1 < n:
+                self._pre(i + 1)
+        self._head()
+        self._sample()
+        return hs, self.logits.float().cpu()
 
     def generate(self, n_steps):
         """n decode steps (greedy, or sampled after set_sampling) from the
         current device state (no host sync)."""
+        if self._host_pos + n_steps > self.max_seq_len:
+            raise ValueError(f"{n_steps} decode steps from position {self._host_pos} exceed "
+                             f"max_seq_len={self.max_seq_len}")
         for _ in range(n_steps):
             self.step()
 

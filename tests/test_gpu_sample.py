@@ -35,9 +35,10 @@ class Sampler:
     def __call__(self, logits, T, top_p, rp=1.0, slot=0, window=0, seed=7):
         hist = self.hist
         rc = self.lib.qh_sample_top_p(
-            abi.ptr(logits), self.V, T, top_p, rp, abi.ptr(hist) if hist is not None else None, None,
-            slot, 0, None, window, seed, abi.ptr(self.ctr), abi.ptr(self.ws), abi.ptr(self.tok), None,
-            None, 0, abi.ptr(self.info), abi.stream_handle())
+            abi.ptr(logits), self.V, T, top_p, rp, abi.ptr(hist) if hist is not None else None,
+            hist.numel() if hist is not None else 0, None, slot, 0, None, window, seed,
+            abi.ptr(self.ctr), abi.ptr(self.ws), abi.ptr(self.tok), None, None, 0,
+            abi.ptr(self.info), abi.stream_handle())
         abi.check(rc, "sample")
         torch.cuda.synchronize()
         info = self.info.cpu().tolist()

@@ -219,3 +219,42 @@ def test_prefill_close_to_sequential_decode():
     a = orc.OracleModel(w, 64, prefill="reference").forward(prompt, 0).view(-1)
     b = orc.OracleModel(w, 64, prefill="sequential").forward(prompt, 0).view(-1)
     assert cos_sim(a, b) > 0.999
+
+
+def test_prefill_continues_from_cache():
+    """A prompt prefilled in two pieces (the second at past_len > 0, which
+    continues from the stored KV cache, conv state and recurrent state,
+    main.py:1130-1131) gives the logits of the one-piece prefill; the
+    recurrent GatedDeltaNet part is the same computation token by token."""
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    cfg = pkg.config.tiny(num_layers=4)
+    w = pkg.synth.make_weights(cfg, seed=0)
+    prompt = pkg.synth.make_prompt(cfg, n=12, seed=3)
+    m = orc.OracleModel(w, 64, prefill="reference")
+    whole = m.forward(prompt, 0, logits_to_keep=0)
+    assert whole.shape == (12, cfg.vocab_size)
+    first = m.forward(prompt[:7], 0, logits_to_keep=0)
+    second = m.forward(prompt[7:], 7, logits_to_keep=0)
+    pieces = torch.cat([first, second])
+    for j in range(12):
+        assert cos_sim(pieces[j], whole[j]) > 0.9999, j
+    # logits_to_keep=k keeps the last k rows of the same computation
+    last2 = m.forward(prompt, 0, logits_to_keep=2)
+    assert torch.equal(last2, whole[-2:])
+
+
+def test_forward_at_zero_starts_a_new_sequence():
+    """forward(ids, 0) ignores whatever an earlier sequence left in the
+    caches: the same prompt gives the same logits after another prompt."""
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    cfg = pkg.config.tiny(num_layers=4)
+    w = pkg.synth.make_weights(cfg, seed=0)
+    a = pkg.synth.make_prompt(cfg, n=5, seed=4)
+    b = pkg.synth.make_prompt(cfg, n=1, seed=5)
+    for mode in ("reference", "sequential"):
+        m = orc.OracleModel(w, 64, prefill=mode)
+        fresh = m.forward(b, 0)
+        m.forward(a, 0)
+        assert torch.equal(m.forward(b, 0), fresh), mode
