@@ -184,6 +184,22 @@ int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_strid
                    const int* pos_dev, int pos, int nsplit, void* scratch, unsigned* counters,
                    void* out, float eps, qh_stream_t stream);
 
+/* Allocation-free variant of qh_attn_decode, same arguments without scratch
+ * and counters.  No counterpart in the reference; it is for callers that
+ * cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): the split partials and arrival counters live in a fixed
+ * library array (4 MiB + 256 bytes per GPU, held until the process ends).
+ * Limits: n_kv <= 64, nsplit 1..64, n_kv * nsplit * 4 * (head_dim + 2) <= 2^20
+ * floats; larger shapes return -1.  The first call on a device looks up the
+ * array's address (make it outside graph capture).  Every call on one GPU
+ * shares the array: calls that overlap on one GPU race. */
+int qh_attn_decode_noalloc(const void* q, int q_stride, const void* gate, int gate_stride,
+                           const void* k_new, const void* v_new, const float* q_norm_w,
+                           const float* k_norm_w, const float* cos_t, const float* sin_t,
+                           void* k_cache, void* v_cache, int max_seq, int head_dim, int rot,
+                           int n_heads, int n_kv, const int* pos_dev, int pos, int nsplit,
+                           void* out, float eps, qh_stream_t stream);
+
 /* GatedDeltaNet decode step: causal conv update (4-slot ring indexed by
  * position), gates, l2norm, delta rule (state in place), gated RMSNorm
  * (main.py:1064-1162 with launch_delta_rule_decode semantics).  `core` is an

@@ -66,6 +66,8 @@ NATIVE_SIGNATURES = {
     "qh_attn_scratch_bytes": (_sz, [_i, _i, _i]),
     "qh_attn_decode": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _f, _vp]),
+    "qh_attn_decode_noalloc": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                    _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _f, _vp]),
     "qh_gdn_decode": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "qh_gdn_decode_core": (_i, [_vp] * 10 + [_i] * 5 + [_vp]),

@@ -19,6 +19,9 @@
 // (atomic arrival counter, self-resetting) merges the partial states and
 // applies the output gate.  The new token's K/V come from registers, so no
 // split ever waits on another.
+#include <cstring>
+#include <mutex>
+
 #include "qh_common.h"
 #include "qh_attn.h"
 
@@ -448,6 +451,54 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   if (threadIdx.x == 0) reset_counter(p.counters + kvh);
 }
 
+// ---- fixed scratch of qh_attn_decode_noalloc --------------------------------
+// Words [0, kStaticCounterWords) are the per-KV-head arrival counters (the
+// kernel's last arriver returns each to zero), the rest the split partials.
+// The array is device memory that each GPU the library runs on holds until
+// the process ends; every call on one GPU shares it.
+constexpr int kStaticCounterWords = 64;                       // n_kv <= 64
+constexpr size_t kStaticPartFloats = (size_t)1 << 20;         // 4 MiB of partials
+constexpr size_t kStaticWords = kStaticCounterWords + kStaticPartFloats;
+constexpr int kMaxDevices = 64;
+
+__global__ __launch_bounds__(64) void zero_words_kernel(unsigned* w, int n) {
+  if ((int)threadIdx.x < n) w[threadIdx.x] = 0u;
+}
+
+}  // namespace
+
+static __device__ __align__(256) uint32_t scratch[kStaticWords];
+
+namespace {
+
+std::mutex g_static_mu;
+uint32_t* g_static_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's copy of `scratch`, looked up once per device
+// (with that device current) and its counters cleared by a fill kernel on
+// the caller's stream.  Host code only ever uses this address: the array's
+// name in host code is a stand-in, not a device pointer.
+uint32_t* static_scratch(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    qh_set_error("attn_decode_noalloc: no current device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  if (!g_static_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      qh_set_error("attn_decode_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(64), 0, st, (unsigned*)ptr,
+                       kStaticCounterWords);
+    g_static_ptr[dev] = (uint32_t*)ptr;
+  }
+  return g_static_ptr[dev];
+}
+
 }  // namespace
 
 size_t qh_attn_scratch_floats(int n_kv, int nsplit, int head_dim) {
@@ -486,5 +537,63 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
     hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(256), 0, st, p);
   else
     hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, p);
+  return 0;
+}
+
+// Allocation-free variant of qh_attn_decode: the split partials and arrival
+// counters live in the file-scope array above instead of caller memory.  No
+// counterpart in the reference; for callers that cannot allocate (code under
+// graph capture, serving loops that forbid hipMalloc).  Limits: n_kv <= 64
+// and n_kv * nsplit * 4 * (head_dim + 2) <= 2^20 partial floats (4 MiB).
+// Calls that overlap on one GPU race on the shared array.
+extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
+    const void* q, int q_stride, const void* gate, int gate_stride, const void* k_new,
+    const void* v_new, const float* q_norm_w, const float* k_norm_w, const float* cos_t,
+    const float* sin_t, void* k_cache, void* v_cache, int max_seq, int head_dim, int rot,
+    int n_heads, int n_kv, const int* pos_dev, int pos, int nsplit, void* out, float eps,
+    hipStream_t stream) {
+  if (n_kv < 1 || n_kv > kStaticCounterWords || nsplit < 1 || nsplit > 64 ||
+      (head_dim != 128 && head_dim != 256) ||
+      qh_attn_scratch_floats(n_kv, nsplit, head_dim) > kStaticPartFloats) {
+    qh_set_error("qh_attn_decode_noalloc: n_kv=%d, nsplit=%d, head_dim=%d exceed the fixed "
+                 "scratch (n_kv <= %d, nsplit 1..64, n_kv*nsplit*4*(head_dim+2) <= %zu floats)",
+                 n_kv, nsplit, head_dim, kStaticCounterWords, kStaticPartFloats);
+    return -1;
+  }
+  uint32_t* ws = static_scratch(stream);
+  if (!ws) return -1;
+  QhAttnParams a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q;
+  a.q_stride = q_stride;
+  a.gate = (const uint16_t*)gate;
+  a.gate_stride = gate_stride;
+  a.k_new = (const uint16_t*)k_new;
+  a.v_new = (const uint16_t*)v_new;
+  a.q_norm_w = q_norm_w;
+  a.k_norm_w = k_norm_w;
+  a.cos_t = cos_t;
+  a.sin_t = sin_t;
+  a.k_cache = (uint16_t*)k_cache;
+  a.v_cache = (uint16_t*)v_cache;
+  a.max_seq = max_seq;
+  a.rot = rot;
+  a.n_heads = n_heads;
+  a.n_kv = n_kv;
+  a.pos_dev = pos_dev;
+  a.rope_pos = pos;
+  a.slot = pos;
+  a.total = pos + 1;
+  a.nsplit = nsplit;
+  a.counters = (unsigned*)ws;
+  a.part = (float*)(ws + kStaticCounterWords);
+  a.out = (uint16_t*)out;
+  a.eps = eps;
+  if (qh_launch_attn(a, head_dim, stream) != 0) return -1;
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    qh_set_error("qh_attn_decode_noalloc: launch failed: %s", hipGetErrorString(e));
+    return -1;
+  }
   return 0;
 }
