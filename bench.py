@@ -5,7 +5,8 @@
 Workload: a Qwen3.5-4B-shaped model (32 layers: 24 GatedDeltaNet + 8 gated
 full-attention, hidden 2560, MLP 9216, vocab 248320, E4M3 128x128
 block-scaled linears with fp32 scale_inv, bf16 embeddings / norms / lm_head),
-random-init from a fixed seed (no checkpoint exists here), a 128-token
+random-init from a seeded CPU torch.Generator and copied to the GPU (no
+checkpoint exists here), a 128-token
 uniform-random prompt, then `warmup` untimed and `steps` timed greedy decode
 steps, each one replay of the captured HIP graph of a full decode step
 (token, position and hidden state stay on the device; no host sync inside the
@@ -18,9 +19,16 @@ Also reported on the same JSON line:
                achieved = algorithmic bytes per launch / mean launch time.
   cpu_baseline the CPU oracle (PyTorch explicit block dequant + fp32 matmul,
                the reference's CPU-equivalent path) on the host cores, timed
-               on a bounded sample of decode steps of the same model.
-  parity       greedy tokens of the GPU engine vs the CPU oracle on a short
-               prompt (the oracle is the checker here, never the product).
+               on a bounded sample (32 decode steps) of the same model, with
+               the host CPU as lscpu reports it.
+  parity       config 5 at full size: the bench prompt through the batch
+               prefill, then --parity-steps (300) greedy steps of the CPU
+               oracle, the GPU engine fed the same tokens (logit cosine and
+               argmax at every position), and the GPU's own free-running
+               tokens against the oracle's (the oracle is the checker here,
+               never the product).
+  memory       torch's allocated and peak allocated GB after the timed decode
+               (the reference harness's last two lines).
   prefill      wall time of the batch prefill of the prompt.
   prefill_gemm BASELINE configs[2] FP8 GEMMs on the matrix cores.
   kernels      BASELINE configs 1, 2, 3b, 4a, 4b kernel by kernel over input
@@ -428,68 +436,126 @@ def kernel_configs(eng, cpu=True):
     return res
 
 
-def cpu_baseline(w_gpu, n_prompt=4, n_steps=8):
-    """CPU oracle decode on the host cores.  Returns (tok/s over the timed
-    greedy steps, threads, setup seconds, prompt, oracle tokens, oracle logits
-    per generated position)."""
+def host_cpu():
+    """The host's CPU as lscpu reports it (model, sockets, physical cores)."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info.update({"model": kv.get("Model name"), "sockets": sockets,
+                     "physical_cores": sockets * per if sockets and per else None,
+                     "threads_per_core": kv.get("Thread(s) per core")})
+    except (OSError, ValueError):
+        pass
+    return info
+
+
+def _bf16_ulp(x):
+    return 2.0 ** (float(torch.floor(torch.log2(x.abs()))) - 7)
+
+
+def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
+    """Config-5 greedy parity on the full model: the CPU oracle (explicit E4M3
+    block dequant, fp32 matmul; the checker, never the product) prefills the
+    prompt through the reference's batch path and decodes greedily for
+    n_steps; the GPU engine is fed the same tokens (teacher forcing) and its
+    logits are compared at every position (cosine; argmax wherever the
+    oracle's top-2 margin exceeds one bf16 ulp of its top logit).  The GPU's
+    own free-running greedy tokens from the same prompt are compared with the
+    oracle's.  The oracle stops early once budget_s seconds have passed.  The
+    first n_timed oracle decode steps are the CPU baseline sample."""
     from oracle import qwen35_oracle as orc
-    from qwen35_amd import synth
-    torch.set_num_threads(os.cpu_count() or 1)
-    w_cpu = w_gpu.to("cpu")
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
     t0 = time.perf_counter()
-    model = orc.OracleModel(w_cpu, max_seq_len=64, prefill="reference")
+    ref = orc.OracleModel(w_cpu, max_seq_len=len(prompt) + n_steps + 1, prefill="reference")
     setup = time.perf_counter() - t0
     log(f"cpu oracle ready ({setup:.0f} s)")
-    prompt = synth.make_prompt(w_cpu.cfg, n=n_prompt, seed=7)
-    logits = model.forward(prompt, 0).view(-1)
-    toks, all_logits = [], [logits]
-    pos = n_prompt
-    t0 = time.perf_counter()
-    for _ in range(n_steps):
-        t = orc.argmax_first(logits)
-        toks.append(t)
-        logits, _ = model.decode_token(t, pos)
-        logits = logits.view(-1)
-        log(f"cpu step {pos - n_prompt + 1}/{n_steps}")
-        all_logits.append(logits)
-        pos += 1
-    dt = time.perf_counter() - t0
-    return n_steps / dt, torch.get_num_threads(), setup, prompt, toks, all_logits
-
-
-def teacher_forced_parity(eng, prompt, o_toks, o_logits):
-    """Feed the oracle's greedy tokens to the GPU engine and compare the
-    logits at every position: cosine, and argmax agreement at positions whose
-    oracle top-1/top-2 margin exceeds one bf16 ulp of the top logit."""
-    eng._reset_cache()
-    g_logits = [eng.forward(prompt.view(1, -1).cuda(), 0).float().cpu().view(-1).clone()]
+    # GPU free-running greedy tokens from the same prompt
+    eng.forward(prompt.view(1, -1).cuda(), 0)
+    eng.generate(n_steps - 1)
+    torch.cuda.synchronize()
+    g_free = eng.tokens(len(prompt) - 1, len(prompt) - 1 + n_steps).cpu().tolist()
+    t_start = time.perf_counter()
+    o_logits = ref.forward(prompt, 0).view(-1)
+    g_logits = eng.forward(prompt.view(1, -1).cuda(), 0).float().cpu().view(-1)
+    prefill_s = time.perf_counter() - t_start
+    rows, o_toks, step_s = [], [], []
     pos = len(prompt)
-    for t in o_toks:
-        g_logits.append(eng.forward(torch.tensor([[t]], device="cuda"), pos).float().cpu().view(-1)
-                        .clone())
-        pos += 1
-    cos, agree, decided, margins = [], 0, 0, []
-    for g, o in zip(g_logits, o_logits):
-        cos.append(float(torch.nn.functional.cosine_similarity(g, o.float(), dim=0)))
-        top = torch.topk(o.float(), 2)
+
+    def compare(g, o):
+        top = torch.topk(o, 2)
         margin = float(top.values[0] - top.values[1])
-        margins.append(round(margin, 5))
-        ulp = 2.0 ** (torch.floor(torch.log2(top.values[0].abs())).item() - 7)
-        if margin > ulp:
-            decided += 1
-            agree += int(int(torch.argmax(g)) == int(top.indices[0]))
-    return {"positions": len(g_logits), "min_logit_cosine": round(min(cos), 7),
-            "argmax_agree_where_margin_gt_1ulp": f"{agree}/{decided}", "top2_margins": margins}
+        decided = margin > _bf16_ulp(top.values[0])
+        agree = int(torch.argmax(g)) == int(top.indices[0])
+        cos = float(torch.nn.functional.cosine_similarity(g.double(), o.double(), dim=0))
+        rows.append((cos, decided, agree, margin))
+
+    compare(g_logits, o_logits.float())
+    deadline = time.perf_counter() + budget_s
+    for k in range(n_steps):
+        t = orc.argmax_first(o_logits)
+        o_toks.append(t)
+        if k == n_steps - 1 or time.perf_counter() > deadline:
+            break
+        ts = time.perf_counter()
+        o_logits = ref.decode_token(t, pos)[0].view(-1)
+        step_s.append(time.perf_counter() - ts)
+        g_logits = eng.forward(torch.tensor([[t]], device="cuda"), pos).float().cpu().view(-1)
+        compare(g_logits, o_logits.float())
+        pos += 1
+        if (k + 1) % 25 == 0:
+            log(f"parity step {k + 1}/{n_steps}: min cosine so far "
+                f"{min(r[0] for r in rows):.6f}")
+    n = len(o_toks)
+    first_diff = next((i for i in range(n) if g_free[i] != o_toks[i]), None)
+    decided = [r for r in rows if r[1]]
+    timed = step_s[:n_timed]
+    out = {
+        "prompt_tokens": len(prompt), "steps": n, "requested_steps": n_steps,
+        "free_running_identical_steps": n if first_diff is None else first_diff,
+        "free_running_first_difference": None if first_diff is None else {
+            "step": first_diff, "gpu_token": g_free[first_diff], "oracle_token": o_toks[first_diff],
+            "oracle_top2_margin": round(rows[first_diff][3], 6)},
+        "teacher_forced": {
+            "positions": len(rows),
+            "min_logit_cosine": round(min(r[0] for r in rows), 7),
+            "mean_logit_cosine": round(sum(r[0] for r in rows) / len(rows), 7),
+            "argmax_agree_where_margin_gt_1ulp": f"{sum(r[2] for r in decided)}/{len(decided)}",
+            "argmax_agree_all_positions": f"{sum(r[2] for r in rows)}/{len(rows)}",
+            "disagreements": [{"position": i, "margin": round(r[3], 6)}
+                              for i, r in enumerate(rows) if not r[2]],
+        },
+        "oracle": "CPU explicit-dequant restatement (oracle/qwen35_oracle.py), batch prefill path",
+        "oracle_prefill_s": round(prefill_s, 1),
+        "oracle_decode_s_per_token": round(sum(step_s) / max(1, len(step_s)), 3),
+    }
+    cpu = {"value": round(len(timed) / sum(timed), 4) if timed else None, "unit": "tok/s",
+           "cores": torch.get_num_threads(), "kind": "port",
+           "sample": f"{len(timed)} greedy decode steps of the same 4B-shaped model at context "
+                     f"{len(prompt)}..{len(prompt) + len(timed)}, CPU oracle (explicit E4M3 block "
+                     f"dequant, fp32 matmul, weights pre-dequantized in {setup:.0f}s)",
+           "host": host_cpu()}
+    return out, cpu
 
 
 def main():
+    t_main = time.perf_counter()
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU oracle (no cpu_baseline, no parity, no CPU kernel timings)")
+    ap.add_argument("--parity-steps", type=int, default=300,
+                    help="greedy steps of the full-size parity run against the CPU oracle")
+    ap.add_argument("--parity-budget", type=float, default=240.0,
+                    help="seconds of oracle decode after which the parity run stops early")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run eager gate/up launches + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--kernels-only", action="store_true",
@@ -522,10 +588,14 @@ def main():
         return
 
     cfg = config.qwen35_4b()
-    w = synth.make_weights(cfg, seed=args.seed, device="cuda")
-    log("weights built")
+    t0 = time.perf_counter()
+    # seeded CPU generator, then copied: the CPU oracle and the GPU see the same bits
+    w_cpu = synth.make_weights(cfg, seed=args.seed, device="cpu")
+    w = w_cpu.to("cuda")
+    log(f"weights built on the CPU generator and copied ({time.perf_counter() - t0:.0f} s)")
     max_seq = 4096
     assert args.prompt + args.warmup + args.steps + 1 <= max_seq
+    torch.cuda.reset_peak_memory_stats()
     eng = engine.Qwen35FP8Engine(w, max_seq_len=max_seq)
     if args.traffic_probe:
         traffic_probe(eng)
@@ -533,13 +603,13 @@ def main():
     if args.kernels_only:
         print(json.dumps({"kernels": kernel_configs(eng, cpu=not args.no_cpu_baseline)}))
         return
+    prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1)
     if args.prefill_probe:
-        prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
-        print(json.dumps({"prefill_probe": True, **time_prefill(eng, prompt)}))
+        print(json.dumps({"prefill_probe": True, **time_prefill(eng, prompt.cuda())}))
         return
     if args.decode_probe:
         # context ~300 like the timed steps: a 300-token prompt, then eager steps
-        eng.prefill(synth.make_prompt(cfg, n=300, seed=args.seed + 1, device="cuda").view(1, -1))
+        eng.prefill(synth.make_prompt(cfg, n=300, seed=args.seed + 1).view(1, -1).cuda())
         for _ in range(3):
             eng.step()
         torch.cuda.synchronize()
@@ -553,8 +623,7 @@ def main():
         return
     eng.capture()
     log("decode step captured")
-    prompt = synth.make_prompt(cfg, n=args.prompt, seed=args.seed + 1, device="cuda")
-    eng.prefill(prompt.view(1, -1))
+    eng.prefill(prompt.view(1, -1).cuda())
     eng.generate(args.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -562,7 +631,10 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     toks_per_s = args.steps / dt
-    log(f"timed decode: {toks_per_s:.1f} tok/s")
+    # the reference harness's memory lines (_benchmark_native_fp8.py:42-43)
+    mem = {"allocated_gb": round(torch.cuda.memory_allocated() / 1e9, 3),
+           "peak_allocated_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3)}
+    log(f"timed decode: {toks_per_s:.1f} tok/s; memory {mem}")
     ms_per_step = dt * 1e3 / args.steps
     ctx0 = args.prompt + args.warmup
     bytes_tok = w.nbytes_per_token()
@@ -573,32 +645,26 @@ def main():
     traffic, tk = measured_traffic()
     traffic_src = (f"profiles/gate_up_traffic_pmc.json ({tk})" if traffic is not None else None)
     achieved = mbytes / (mlp_us * 1e-6) / 1e9
-    prefill = time_prefill(eng, prompt)
+    prefill = time_prefill(eng, prompt.cuda())
     log(f"prefill: {prefill['prompt_tokens']} tokens in {prefill['ms']} ms")
     kernels = kernel_configs(eng, cpu=not args.no_cpu_baseline)
     gemm = time_prefill_gemm()
     log("prefill GEMM: " + ", ".join(f"{g['N']}x{g['K']} {g['us']} us ({g['tflops']} TFLOP/s)"
                                      for g in gemm["gemms"]))
 
-    # short greedy parity sample (GPU engine vs CPU oracle, same weights)
+    # config-5 greedy parity at full size (GPU engine vs CPU oracle, same weights)
     cpu = None
     parity = None
-    if not args.no_cpu_baseline:
-        log("cpu baseline (oracle) ...")
-        tps, threads, setup, p_prompt, o_toks, o_logits = cpu_baseline(w)
-        log(f"cpu baseline: {tps:.4f} tok/s on {threads} threads")
-        eng._reset_cache()
-        eng.prefill(p_prompt.view(1, -1).cuda())
-        eng.generate(len(o_toks) - 1)
-        torch.cuda.synchronize()
-        g_toks = eng.tokens(len(p_prompt) - 1, len(p_prompt) - 1 + len(o_toks)).cpu().tolist()
-        parity = {"prompt": len(p_prompt), "steps": len(o_toks), "free_running_gpu_tokens": g_toks,
-                  "free_running_oracle_tokens": o_toks,
-                  "teacher_forced": teacher_forced_parity(eng, p_prompt, o_toks, o_logits)}
-        cpu = {"value": round(tps, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{len(o_toks)} greedy decode steps of the same 4B-shaped model after a "
-                         f"{len(p_prompt)}-token prompt, CPU oracle (explicit E4M3 block dequant, "
-                         f"fp32 matmul, weights pre-dequantized in {setup:.0f}s)"}
+    if not args.no_cpu_baseline and args.parity_steps > 0:
+        log(f"parity: {args.prompt}-token prompt + {args.parity_steps} greedy steps vs the CPU oracle")
+        # the whole run stays under ~9 minutes however fast the host is
+        budget = min(args.parity_budget, max(30.0, 480.0 - (time.perf_counter() - t_main)))
+        parity, cpu = parity_run(eng, w_cpu, prompt, args.parity_steps, budget)
+        tf = parity["teacher_forced"]
+        log(f"parity: {parity['steps']} steps, free-running identical for "
+            f"{parity['free_running_identical_steps']}, teacher-forced min cosine "
+            f"{tf['min_logit_cosine']}, argmax {tf['argmax_agree_where_margin_gt_1ulp']}")
+        log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads")
 
     out = {
         "metric": "batch-1 decode tok/s (300 steps) + FP8 GEMV HBM GB/s vs peak",
@@ -638,6 +704,7 @@ def main():
             "launches_timed": n_launch,
         },
         "cpu_baseline": cpu,
+        "memory": mem,
         "prefill": prefill,
         "prefill_gemm": gemm,
         "kernels": kernels,
