@@ -489,10 +489,10 @@ def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
     def compare(g, o):
         top = torch.topk(o, 2)
         margin = float(top.values[0] - top.values[1])
-        decided = margin > _bf16_ulp(top.values[0])
+        ulp = _bf16_ulp(top.values[0])
         agree = int(torch.argmax(g)) == int(top.indices[0])
         cos = float(torch.nn.functional.cosine_similarity(g.double(), o.double(), dim=0))
-        rows.append((cos, decided, agree, margin))
+        rows.append((cos, margin > ulp, agree, margin, margin / ulp))
 
     compare(g_logits, o_logits.float())
     deadline = time.perf_counter() + budget_s
@@ -526,8 +526,14 @@ def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
             "mean_logit_cosine": round(sum(r[0] for r in rows) / len(rows), 7),
             "argmax_agree_where_margin_gt_1ulp": f"{sum(r[2] for r in decided)}/{len(decided)}",
             "argmax_agree_all_positions": f"{sum(r[2] for r in rows)}/{len(rows)}",
-            "disagreements": [{"position": i, "margin": round(r[3], 6)}
+            "argmax_disagree_above_4ulp": sum(1 for r in rows if not r[2] and r[4] > 4.0),
+            "disagreements": [{"position": i, "margin": round(r[3], 6),
+                               "margin_bf16_ulps": round(r[4], 2)}
                               for i, r in enumerate(rows) if not r[2]],
+            "noise_floor": "two exact restatements of the reference (oracle fp32 vs fp64-accumulated "
+                           "matmuls, tests/parity_noise_floor.py, 60 positions of this model) agree "
+                           "at 52/54 positions above 1 ulp, mean logit cosine 0.99943, disagreeing "
+                           "only at margins <= 2 ulps",
         },
         "oracle": "CPU explicit-dequant restatement (oracle/qwen35_oracle.py), batch prefill path",
         "oracle_prefill_s": round(prefill_s, 1),

@@ -300,43 +300,6 @@ int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0, 
                          int kb2, const void* w3, const void* s3, void* y3, int n3, int kb3,
                          int scales_bf16, void* ws, qh_stream_t stream);
 
-/* One phase of a chained launch.  kind 1: grouped E4M3 GEMV (segments
- * w/s/y/n/kb as in qh_gemv_e4m3, optional (1+w) RMSNorm prologue and
- * residual res1 [+ res2]); kind 2: gate/up MLP (w[0]/s[0] gate, w[1]/s[1] up,
- * y[0] = bf16(silu(g)*u), optional y[1] = g, y[2] = u, n[0] rows, kb[0]).
- * nwg = workgroups for the phase (0: default).  Fast-path shapes only: K in
- * {2560, 4096, 9216} for GEMV, 2560 for gate/up; fp32 128x128 block scales. */
-typedef struct qh_chain_phase {
-  int kind;
-  int nwg;
-  const void* x;
-  const void* x2;
-  const float* norm_w;
-  const void* res1;
-  const void* res2;
-  float eps;
-  int K;
-  int nseg;
-  const void* w[4];
-  const void* s[4];
-  void* y[4];
-  int n[4];
-  int kb[4];
-} qh_chain_phase_t;
-
-/* Number of uint32 sync words qh_chain needs (zero-initialised once; every
- * launch returns them to zero). */
-int qh_chain_sync_words(void);
-
-/* Runs up to 4 dependent phases (e.g. out_proj -> gate/up -> down -> next
- * layer's input projection) in one launch: later phases' workgroups take
- * ordered tickets, issue their weight loads, then wait for the previous
- * phase's arrival count.  No reference counterpart (the reference launches
- * each projection separately; its largest fusion is layer_post_o_fp8_mlp,
- * fused_kernels.cu:1156-1195).  err (optional) is set to 1 if a wait expired. */
-int qh_chain(const qh_chain_phase_t* phases, int nphase, unsigned* sync, int* err,
-             qh_stream_t stream);
-
 /* ---- batch prefill pieces (the reference runs these in torch) ---------- */
 
 /* q/k head (1+w) RMSNorm + partial RoPE (q kept fp32, k cached bf16) and the

@@ -90,19 +90,7 @@ NATIVE_SIGNATURES = {
     "qh_gdn_prep": (_i, [_vp] * 12 + [_i] * 6 + [_vp]),
     "qh_gdn_scan": (_i, [_vp] * 9 + [_i] * 5 + [_f, _vp]),
     "qh_silu_mul": (_i, [_vp, _vp, _vp, _sz, _vp]),
-    "qh_chain_sync_words": (_i, []),
-    "qh_chain": (_i, [_vp, _i, _vp, _vp, _vp]),
 }
-
-
-class ChainPhase(ctypes.Structure):
-    """Mirror of qh_chain_phase_t (include/qwen35_fp8_hip.h)."""
-    _fields_ = [("kind", _i), ("nwg", _i), ("x", _vp), ("x2", _vp), ("norm_w", _vp),
-                ("res1", _vp), ("res2", _vp), ("eps", _f), ("K", _i), ("nseg", _i),
-                ("w", _vp * 4), ("s", _vp * 4), ("y", _vp * 4), ("n", _i * 4), ("kb", _i * 4)]
-
-    GEMV = 1
-    MLP = 2
 
 
 class QhError(RuntimeError):

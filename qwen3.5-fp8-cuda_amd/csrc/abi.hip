@@ -757,20 +757,6 @@ QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const 
   return check_launch("qh_gemm_e4m3_grouped");
 }
 
-// Chained decode phases (no reference counterpart: the reference launches each
-// projection separately, fused_kernels.cu:1156-1195 being its largest fusion).
-// Up to 4 dependent GEMV / gate-up phases in one launch; `sync` holds
-// qh_chain_sync_words() uint32 words, zeroed once before the first launch (the
-// counters only grow; one buffer per call site), `err` (optional) is set to 1
-// if a phase wait expired.
-QH_EXPORT int qh_chain_sync_words(void) { return qh_chain_sync_word_count(); }
-
-QH_EXPORT int qh_chain(const void* phases, int nphase, unsigned* sync, int* err,
-                       hipStream_t stream) {
-  if (qh_launch_chain((const QhChainPhaseDesc*)phases, nphase, sync, err, stream) != 0) return -1;
-  return check_launch("qh_chain");
-}
-
 // ---- batch prefill pieces (the reference runs these in torch) -------------------
 // q/k head norm + partial RoPE (q kept fp32) + KV-cache write for M tokens at
 // positions past.. (main.py:1034-1043).

@@ -73,27 +73,9 @@ __device__ __forceinline__ int out_index(const QhGemvSeg& sg, int row) {
   return w < d ? h * d + w : (sg.n >> 1) + h * d + (w - d);
 }
 
-// ---- coherent activation I/O ----------------------------------------------------
-// Inside one launch of the chained kernel (below), activations pass between
-// workgroups that may sit on different XCDs, whose L2 caches are not coherent
-// with each other: such activations are written and read with sc1
-// (device-scope) buffer operations, which are coherent across the XCDs for
-// that access without any cache maintenance.  Standalone launches use plain
-// accesses (the kernel boundary orders them).
-constexpr int kSc1 = 16;
-template <bool COH>
+// ---- activation I/O -------------------------------------------------------------
 __device__ __forceinline__ u32x4 ld_act8(const uint16_t* base, int elem) {
-  if (COH)
-    return __builtin_amdgcn_raw_buffer_load_b128(make_rsrc(base, kMaxBufferRange), (uint32_t)elem * 2u,
-                                                 0, kSc1);
   return *(const u32x4*)(base + elem);
-}
-template <bool COH>
-__device__ __forceinline__ void st_act1(uint16_t* p, uint16_t v) {
-  if (COH)
-    __builtin_amdgcn_raw_buffer_store_b16(v, make_rsrc(p, 2u), 0, 0, kSc1);
-  else
-    *p = v;
 }
 
 __device__ __forceinline__ u32x4 ld_w16(const uint16_t* p) {
@@ -151,7 +133,7 @@ constexpr bool early_x() { return CPL <= 8; }
 // gw: optional bf16 weights [gd] of a per-head gated RMSNorm (x = the
 // GatedDeltaNet core, x2 = its gate z); a chunk's 8 weights are kept in w0 as
 // raw bits.
-template <int CPL, bool COH = false, int NT = 256>
+template <int CPL, int NT = 256>
 __device__ __forceinline__ void block_x_load(XIn<CPL, NT>& in, const uint16_t* x, const uint16_t* x2,
                                              const float* norm_w, int K, const uint16_t* gw = nullptr,
                                              int gd = 0) {
@@ -161,8 +143,8 @@ __device__ __forceinline__ void block_x_load(XIn<CPL, NT>& in, const uint16_t* x
   for (int i = 0; i < XIn<CPL, NT>::MAXC; ++i) {
     const int c = tid + NT * i;
     const int cc = c < nch ? c : 0;
-    in.v[i] = ld_act8<COH>(x, cc * 8);
-    if (x2) in.v2[i] = ld_act8<COH>(x2, cc * 8);
+    in.v[i] = ld_act8(x, cc * 8);
+    if (x2) in.v2[i] = ld_act8(x2, cc * 8);
     if (gw) {
       in.w0[i] = __builtin_bit_cast(f32x4, *(const u32x4*)(gw + (cc * 8) % gd));
     } else if (norm_w) {
@@ -233,7 +215,7 @@ __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, f
 // Prologue variant for large K: loads and combines x / x2 in one pass and
 // fetches the norm weights only after the sum of squares, so at most MAXC
 // chunks are live while a wave's weight loads are in flight.
-template <int CPL, bool COH = false, int NT = 256>
+template <int CPL, int NT = 256>
 __device__ __forceinline__ void block_x_direct(uint16_t* sx, float* red, const uint16_t* x,
                                                const uint16_t* x2, const float* norm_w, float eps,
                                                int K) {
@@ -246,8 +228,8 @@ __device__ __forceinline__ void block_x_direct(uint16_t* sx, float* red, const u
   for (int i = 0; i < MAXC; ++i) {
     const int c = tid + NT * i;
     const int cc = c < nch ? c : 0;
-    u32x4 a = ld_act8<COH>(x, cc * 8);
-    if (x2) a = add_bf16x8(a, ld_act8<COH>(x2, cc * 8));
+    u32x4 a = ld_act8(x, cc * 8);
+    if (x2) a = add_bf16x8(a, ld_act8(x2, cc * 8));
     v[i] = c < nch ? a : zero;
   }
   if (norm_w) {
@@ -643,66 +625,11 @@ __device__ __forceinline__ void x_arrived(const XIn<CPL, NT>& in) {
   asm volatile("; activation %0" ::"v"(in.v[0].x) : "memory");
 }
 
-// Dependency of a chained phase: wait until *done >= need.  Thread 0 polls
-// with device-scope atomic loads and s_sleep between polls; the rest of the
-// workgroup waits at the barrier.  The wait is bounded: on expiry it flags
-// *err and returns, so every wave always finishes.
-// The count is split over kChainParts 64-bit words, each on its own 128-byte
-// line (stride kChainPartStride words); wave 0's first lanes load one part
-// each and sum them.
-constexpr int kChainParts = 16;
-constexpr int kChainPartStride = 32;
-struct QhWait {
-  unsigned* parts;          // null: no dependency
-  unsigned long long need;  // wait until the parts sum to at least this
-  int* err;
-};
-constexpr unsigned kSpinLimit = 1u << 21;
-
-__device__ __forceinline__ unsigned long long* chain_part(unsigned* parts, int j) {
-  return (unsigned long long*)(parts + kChainPartStride * j);
-}
-// Sum of the kChainParts counters, the same value in all 64 lanes of the
-// calling wave (lanes past kChainParts contribute zero to a full butterfly), so
-// loop conditions on it are wave-uniform.
-__device__ __forceinline__ unsigned long long chain_count(unsigned* parts) {
-  const int lane = threadIdx.x & 63;
-  unsigned long long v = 0;
-  if (lane < kChainParts)
-    v = __hip_atomic_load(chain_part(parts, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ void chain_wait(const QhWait& w) {
-  if (w.parts == nullptr) return;
-  if (threadIdx.x < 64) {
-    unsigned it = 0;
-    while (chain_count(w.parts) < w.need) {
-      __builtin_amdgcn_s_sleep(4);
-      if (++it == kSpinLimit) {
-        if (w.err && (threadIdx.x & 63) == 0)
-          __hip_atomic_store(w.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-// Grouped E4M3 GEMV, one phase's share: workgroup `wg` of `nwg`.
-// CH = false: standalone launch; the activation loads go out first, then the
-//   weight pipeline.
-// CH = true: a dependent phase of the chained kernel; the weight pipeline
-//   (which does not depend on earlier phases) goes out first, then the wait,
-//   then the activation and residual loads (coherent).
-// OUTC: outputs stored coherently (read by later phases of the same launch).
-// NORM: the (1+w) RMSNorm prologue may be requested (p.norm_w); without it the
-//   norm weights take no registers.
-template <int CPL, int P, typename ScaleT, bool CH, bool OUTC = CH, int NT = 256>
+// Grouped E4M3 GEMV, workgroup `wg` of `nwg`: the activation loads go out
+// first, then the weight pipeline.
+template <int CPL, int P, typename ScaleT, int NT = 256>
 __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, int nwg, uint16_t* sx,
-                                               float* red, const QhWait& wt) {
+                                               float* red) {
   constexpr int K = CPL * 512;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -728,28 +655,22 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
     if (p.res1) {
       const bool valid = gg < p.gtotal;
       float v = bf2f(__builtin_amdgcn_raw_buffer_load_b16(make_rsrc(p.res1 + row_, valid ? 2u : 0u), 0,
-                                                          0, CH ? kSc1 : 0));
+                                                          0, 0));
       if (p.res2)
         v = rbf(v + bf2f(__builtin_amdgcn_raw_buffer_load_b16(
-                        make_rsrc(p.res2 + row_, valid ? 2u : 0u), 0, 0, CH ? kSc1 : 0)));
+                        make_rsrc(p.res2 + row_, valid ? 2u : 0u), 0, 0, 0)));
       res_ = v;
     }
   };
   (void)res;
 
   XIn<CPL, NT> xin;
-  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
+  block_x_load<CPL, NT>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
 #pragma unroll
   for (int s = 0; s < P; ++s) {
-    if (!CH && s == fast_lead(CPL)) x_arrived(xin);
+    if (s == fast_lead(CPL)) x_arrived(xin);
     issue_w(w[s], sc[s], srow[s], sseg[s], g + s * stride);
-    if (!CH) issue_res(res[s], srow[s], g + s * stride);
-  }
-  if (CH) {
-    chain_wait(wt);
-    block_x_load<CPL, true, NT>(xin, p.x, p.x2, p.norm_w, K);
-#pragma unroll
-    for (int s = 0; s < P; ++s) issue_res(res[s], srow[s], g + s * stride);
+    issue_res(res[s], srow[s], g + s * stride);
   }
   u32x4 xr[CPL];
   block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
@@ -764,7 +685,7 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
       if (lane == 0) {
         float y = rbf(acc);
         if (p.res1) y = res[s] + y;
-        st_act1<OUTC>(p.seg[sseg[s]].y + out_index(p.seg[sseg[s]], srow[s]), f2bf(y));
+        p.seg[sseg[s]].y[out_index(p.seg[sseg[s]], srow[s])] = f2bf(y);
       }
       issue_w(w[s], sc[s], srow[s], sseg[s], g + P * stride);
       issue_res(res[s], srow[s], g + P * stride);
@@ -773,11 +694,10 @@ __device__ __forceinline__ void gemv_fast_body(const QhGemvParams& p, int wg, in
   }
 }
 
-// Paired gate/up GEMV with the SiLU(g)*u epilogue, one phase's share (see
-// gemv_fast_body for CH).
-template <int CPL, int P, typename ScaleT, bool CH, bool OUTC = CH, int NT = 256>
+// Paired gate/up GEMV with the SiLU(g)*u epilogue, workgroup `wg` of `nwg`.
+template <int CPL, int P, typename ScaleT, int NT = 256>
 __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int nwg, uint16_t* sx,
-                                              float* red, const QhWait& wt) {
+                                              float* red) {
   constexpr int K = CPL * 512;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -787,19 +707,15 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
   int g = wg * NW + wid;
 
   XIn<CPL, NT> xin;
-  if (!CH) block_x_load<CPL, false, NT>(xin, p.x, p.x2, p.norm_w, K);
+  block_x_load<CPL, NT>(xin, p.x, p.x2, p.norm_w, K);
   u32x2 wg_[P][CPL], wu[P][CPL];
   float sg[P][scale_regs<CPL>()], su[P][scale_regs<CPL>()];
 #pragma unroll
   for (int s = 0; s < P; ++s) {
-    if (!CH && s == mlp_fast_lead(CPL)) x_arrived(xin);
+    if (s == mlp_fast_lead(CPL)) x_arrived(xin);
     const int gg = g + s * stride;
     issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gg, gg < p.N, lw, lane);
     issue_fast<CPL, ScaleT>(wu[s], su[s], p.wu, p.su, gg, gg < p.N, lw, lane);
-  }
-  if (CH) {
-    chain_wait(wt);
-    block_x_load<CPL, true, NT>(xin, p.x, p.x2, p.norm_w, K);
   }
   u32x4 xr[CPL];
   block_x_finish<CPL, NT>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
@@ -813,9 +729,9 @@ __device__ __forceinline__ void mlp_fast_body(const QhMlpParams& p, int wg, int 
       const float au = wave_total(dot_row<CPL>(wu[s], su[s], xr, q4));
       if (lane == 0) {
         // SiLU on the fp32 accumulators (fused_kernels.cu:476).
-        st_act1<OUTC>(p.m_out + g, f2bf(qh_silu(ag) * au));
-        if (p.g_out) st_act1<OUTC>(p.g_out + g, f2bf(ag));
-        if (p.u_out) st_act1<OUTC>(p.u_out + g, f2bf(au));
+        p.m_out[g] = f2bf(qh_silu(ag) * au);
+        if (p.g_out) p.g_out[g] = f2bf(ag);
+        if (p.u_out) p.u_out[g] = f2bf(au);
       }
       const int gn = g + P * stride;
       issue_fast<CPL, ScaleT>(wg_[s], sg[s], p.wg, p.sg, gn, gn < p.N, lw, lane);
@@ -834,8 +750,7 @@ __global__ __launch_bounds__(NT)
 __attribute__((amdgpu_waves_per_eu(2))) void gemv_fast_kernel(QhGemvParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[NT / 64];
-  const QhWait none = {nullptr, 0ull, nullptr};
-  gemv_fast_body<CPL, P, ScaleT, false, false, NT>(p, blockIdx.x, gridDim.x, sx, red, none);
+  gemv_fast_body<CPL, P, ScaleT, NT>(p, blockIdx.x, gridDim.x, sx, red);
 }
 
 template <int CPL, int P, typename ScaleT, int NT = 256>
@@ -843,90 +758,7 @@ __global__ __launch_bounds__(NT)
 __attribute__((amdgpu_waves_per_eu(2))) void mlp_fast_kernel(QhMlpParams p) {
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[NT / 64];
-  const QhWait none = {nullptr, 0ull, nullptr};
-  mlp_fast_body<CPL, P, ScaleT, false, false, NT>(p, blockIdx.x, gridDim.x, sx, red, none);
-}
-
-// ---- chained decode phases ------------------------------------------------------
-// One launch runs up to kChainMaxPhases dependent GEMV / gate-up phases (for
-// example out_proj -> gate/up -> down -> next layer's input projection) on a
-// persistent grid: every workgroup takes part in every phase, and the grid is
-// sized to be resident at once (occupancy x CUs, checked by the launcher), so
-// the waits below always end.  Between phases a workgroup signals that it has
-// finished phase k-1, issues its first phase-k weight loads, and only then
-// waits for all workgroups to finish phase k-1 before it reads the new
-// activation: the next phase's weights stream in while the previous phase
-// drains, with no kernel boundary in between.
-//
-// Synchronisation: phase k's finished-workgroup count lives in kChainParts
-// 64-bit words (one 128-byte line each, so no two atomics or polls share an
-// address); a finishing workgroup adds 1 to part (blockIdx % kChainParts)
-// without waiting for the result.  Counts only grow over launches: at its
-// start a workgroup derives the launch epoch e as floor(count of the last
-// phase / grid) -- exact, since that workgroup has not finished the last phase
-// of this launch -- and phase k waits for count(k-1) >= (e+1) * grid.  The
-// buffer is zeroed once and belongs to one call site (fixed phases and grid).
-constexpr int kChainMaxPhases = 4;
-constexpr int kChainSyncWords = kChainPartStride * kChainParts * kChainMaxPhases;
-enum { kPhGemv = 1, kPhMlp = 2 };
-
-struct QhChainParams {
-  int nphase;
-  int kind[kChainMaxPhases];
-  int cpl[kChainMaxPhases];
-  QhGemvParams g[kChainMaxPhases];
-  QhMlpParams m[kChainMaxPhases];
-  unsigned* sync;
-  int* err;  // set to 1 if a wait expired
-};
-
-__device__ __forceinline__ unsigned* chain_phase_parts(unsigned* sync, int k) {
-  return sync + kChainPartStride * kChainParts * k;
-}
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void chain_kernel(QhChainParams c) {
-  __shared__ __align__(16) uint16_t sx[18 * 512];
-  __shared__ float red[4];
-  __shared__ unsigned long long s_epoch;
-  const int wg = blockIdx.x, nwg = gridDim.x;
-  if (c.nphase > 1) {
-    if (threadIdx.x < 64) {
-      const unsigned long long n = chain_count(chain_phase_parts(c.sync, c.nphase - 1));
-      if (threadIdx.x == 0) s_epoch = n / (unsigned)nwg;
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int k = 0; k < kChainMaxPhases; ++k) {
-    if (k >= c.nphase) break;
-    if (k == 0) {
-      // No dependency: the standalone order (activation loads first), plain
-      // inputs (written by earlier launches), coherent outputs.
-      const QhWait none = {nullptr, 0ull, nullptr};
-      switch (c.kind[0] * 64 + c.cpl[0]) {
-        case kPhGemv * 64 + 5: gemv_fast_body<5, 4, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
-        case kPhGemv * 64 + 8: gemv_fast_body<8, 1, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
-        case kPhGemv * 64 + 18: gemv_fast_body<18, 1, float, false, true>(c.g[0], wg, nwg, sx, red, none); break;
-        case kPhMlp * 64 + 5: mlp_fast_body<5, 2, float, false, true>(c.m[0], wg, nwg, sx, red, none); break;
-        default: break;
-      }
-    } else {
-      const QhWait wt = {chain_phase_parts(c.sync, k - 1), (s_epoch + 1ull) * (unsigned)nwg, c.err};
-      switch (c.kind[k] * 64 + c.cpl[k]) {
-        case kPhGemv * 64 + 5: gemv_fast_body<5, 4, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
-        case kPhGemv * 64 + 8: gemv_fast_body<8, 1, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
-        case kPhGemv * 64 + 18: gemv_fast_body<18, 1, float, true>(c.g[k], wg, nwg, sx, red, wt); break;
-        case kPhMlp * 64 + 5: mlp_fast_body<5, 2, float, true>(c.m[k], wg, nwg, sx, red, wt); break;
-        default: break;
-      }
-    }
-    // Signal phase k once this workgroup's stores have completed.
-    wait_mem();
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(chain_part(chain_phase_parts(c.sync, k), wg % kChainParts), 1ull,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  mlp_fast_body<CPL, P, ScaleT, NT>(p, blockIdx.x, gridDim.x, sx, red);
 }
 
 // ---- bf16 lm_head GEMV + greedy argmax -------------------------------------
@@ -1240,117 +1072,6 @@ int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st) {
 #undef M
   return 0;
 }
-
-int qh_launch_chain(const QhChainPhaseDesc* ph, int nphase, unsigned* sync, int* err,
-                    hipStream_t st) {
-  if (nphase < 1 || nphase > kChainMaxPhases) {
-    qh_set_error("chain: nphase=%d outside [1, %d]", nphase, kChainMaxPhases);
-    return -1;
-  }
-  if (ph == nullptr || sync == nullptr) {
-    qh_set_error("chain: null phase table or sync buffer");
-    return -1;
-  }
-  QhChainParams c = {};
-  c.nphase = nphase;
-  c.sync = sync;
-  c.err = err;
-  for (int k = 0; k < nphase; ++k) {
-    const QhChainPhaseDesc& d = ph[k];
-    if (d.K <= 0 || d.K % 512 != 0) {
-      qh_set_error("chain: phase %d: K=%d is not a multiple of 512", k, d.K);
-      return -1;
-    }
-    const int cpl = d.K / 512;
-    if (d.kind == kPhGemv) {
-      if (cpl != 5 && cpl != 8 && cpl != 18) {
-        qh_set_error("chain: phase %d: GEMV K=%d unsupported (2560, 4096, 9216)", k, d.K);
-        return -1;
-      }
-      if (d.nseg < 1 || d.nseg > 4) {
-        qh_set_error("chain: phase %d: nseg=%d outside [1, 4]", k, d.nseg);
-        return -1;
-      }
-      QhGemvParams& p = c.g[k];
-      p.x = (const uint16_t*)d.x;
-      p.x2 = (const uint16_t*)d.x2;
-      p.norm_w = d.norm_w;
-      p.res1 = (const uint16_t*)d.res1;
-      p.res2 = (const uint16_t*)d.res2;
-      p.eps = d.eps;
-      p.K = d.K;
-      p.nseg = d.nseg;
-      p.gstart[0] = 0;
-      for (int i = 0; i < d.nseg; ++i) {
-        if (d.w[i] == nullptr || d.s[i] == nullptr || d.y[i] == nullptr || d.n[i] <= 0) {
-          qh_set_error("chain: phase %d segment %d: null pointer or n <= 0", k, i);
-          return -1;
-        }
-        if (d.kb[i] != d.K / 128 || (uint64_t)d.n[i] * (uint64_t)d.K > kMaxBufferBytes) {
-          qh_set_error("chain: phase %d segment %d: needs 128x128 block scales (kb=%d) and < 2^31 "
-                       "bytes", k, i, d.K / 128);
-          return -1;
-        }
-        p.seg[i].w = (const uint8_t*)d.w[i];
-        p.seg[i].s = d.s[i];
-        p.seg[i].y = (uint16_t*)d.y[i];
-        p.seg[i].n = d.n[i];
-        p.seg[i].kb = d.kb[i];
-        p.gstart[i + 1] = p.gstart[i] + d.n[i];
-      }
-      for (int i = d.nseg + 1; i < 5; ++i) p.gstart[i] = p.gstart[d.nseg];
-      p.gtotal = p.gstart[d.nseg];
-    } else if (d.kind == kPhMlp) {
-      if (cpl != 5) {
-        qh_set_error("chain: phase %d: gate/up K=%d unsupported (2560)", k, d.K);
-        return -1;
-      }
-      if (d.w[0] == nullptr || d.w[1] == nullptr || d.s[0] == nullptr || d.s[1] == nullptr ||
-          d.y[0] == nullptr || d.n[0] <= 0 || d.kb[0] != d.K / 128 ||
-          (uint64_t)d.n[0] * (uint64_t)d.K > kMaxBufferBytes) {
-        qh_set_error("chain: phase %d: gate/up needs w[0..1], s[0..1], y[0], n[0] > 0 and 128x128 "
-                     "block scales", k);
-        return -1;
-      }
-      QhMlpParams& m = c.m[k];
-      m.x = (const uint16_t*)d.x;
-      m.x2 = (const uint16_t*)d.x2;
-      m.norm_w = d.norm_w;
-      m.eps = d.eps;
-      m.K = d.K;
-      m.wg = (const uint8_t*)d.w[0];
-      m.sg = d.s[0];
-      m.wu = (const uint8_t*)d.w[1];
-      m.su = d.s[1];
-      m.N = d.n[0];
-      m.kb = d.kb[0];
-      m.m_out = (uint16_t*)d.y[0];
-      m.g_out = (uint16_t*)d.y[1];
-      m.u_out = (uint16_t*)d.y[2];
-    } else {
-      qh_set_error("chain: phase %d: unknown kind %d", k, d.kind);
-      return -1;
-    }
-    if (d.x == nullptr) {
-      qh_set_error("chain: phase %d: null activation", k);
-      return -1;
-    }
-    c.kind[k] = d.kind;
-    c.cpl[k] = cpl;
-  }
-  // A persistent grid: every workgroup must be resident at once.  ph[0].nwg
-  // may ask for fewer; never more.
-  const int cap = resident_blocks((const void*)chain_kernel);
-  const int grid = ph[0].nwg > 0 ? ph[0].nwg : cap;
-  if (grid > cap) {
-    qh_set_error("chain: %d workgroups exceed the %d that fit on the device at once", grid, cap);
-    return -1;
-  }
-  hipLaunchKernelGGL(chain_kernel, dim3(grid), dim3(256), 0, st, c);
-  return 0;
-}
-
-int qh_chain_sync_word_count() { return kChainSyncWords; }
 
 int qh_lm_head_grid(int N) {
   const int ng = (N + 3) / 4;

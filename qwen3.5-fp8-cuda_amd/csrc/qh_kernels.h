@@ -76,32 +76,7 @@ struct QhLmHeadParams {
   uint16_t* embed_out;    // ... into this [K] buffer for the next step
 };
 
-// One phase of a chained launch (same layout as qh_chain_phase_t in the public
-// header).  kind 1: grouped GEMV (w/s/y/n/kb per segment, optional residual);
-// kind 2: gate/up MLP (w[0], s[0] gate; w[1], s[1] up; y[0] = bf16(silu(g)*u),
-// optional y[1] = g, y[2] = u; n[0] rows; kb[0]).
-struct QhChainPhaseDesc {
-  int kind;
-  int nwg;
-  const void* x;
-  const void* x2;
-  const float* norm_w;
-  const void* res1;
-  const void* res2;
-  float eps;
-  int K;
-  int nseg;
-  const void* w[4];
-  const void* s[4];
-  void* y[4];
-  int n[4];
-  int kb[4];
-};
-
 int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st);
-int qh_launch_chain(const QhChainPhaseDesc* ph, int nphase, unsigned* sync, int* err,
-                    hipStream_t st);
-int qh_chain_sync_word_count();
 int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st);
 int qh_launch_lm_head(QhLmHeadParams p, int grid, hipStream_t st);
 int qh_lm_head_grid(int N);

@@ -16,16 +16,7 @@ Per decode step the GPU runs 5 kernels per layer plus one for the head:
                    position += 1, next token's embedding row.
 Token, position and hidden state stay on the device, so one step is a
 replayable HIP graph with no host round trip.
-
-With use_chain=True (4B shapes only) the launches between two mixers run as
-one chained launch (qh_chain: output projection, gate/up, down, next input
-projection on a persistent grid with device-side phase barriers).  It gives
-bit-identical results but measured slower on MI355X (45.6 vs 33.3 us per
-layer): a grid-wide barrier across the non-coherent per-XCD L2s costs more
-than the kernel boundary it replaces, so separate launches are the default.
 """
-import ctypes
-import math
 
 import torch
 
@@ -54,7 +45,7 @@ def default_attn_splits(max_seq):
 
 class Qwen35FP8Engine:
     def __init__(self, weights, max_seq_len=4096, attn_splits=None, device="cuda",
-                 use_chain=False, batch_prefill=True, split_gdn=True):
+                 batch_prefill=True, split_gdn=True):
         if not torch.cuda.is_available():
             raise RuntimeError("Qwen35FP8Engine needs a GPU (there is no CPU fallback)")
         self.lib = abi.load()
@@ -120,22 +111,13 @@ class Qwen35FP8Engine:
         self.prompt_buf = None
         self.batch_prefill = batch_prefill
         self._pf = None          # prefill buffers, sized for the longest prompt seen
-        # Chained launches (qh_chain): per layer, the mixer's output projection,
-        # gate/up, down and the next layer's input projection run as one launch.
-        self.use_chain = use_chain and self._chain_shapes_ok()
         # GatedDeltaNet decode split in two launches' worth of work: the step up
         # to the bf16 core (qh_gdn_decode_core, one wave per head and 8 value
         # columns), then the gated RMSNorm as the output projection's prologue
         # (qh_gemv_e4m3_gated).  Needs head dims 128, Hv % 8 == 0 and the fast
-        # GEMV shape for out_proj; the chained path keeps the fused step.
-        self.split_gdn = split_gdn and not self.use_chain and self._split_gdn_ok()
+        # GEMV shape for out_proj; other shapes run the fused step.
+        self.split_gdn = split_gdn and self._split_gdn_ok()
         self.gdn_core = torch.zeros(cfg.value_dim, **bf)
-        if self.use_chain:
-            words = int(self.lib.qh_chain_sync_words())
-            self.chain_sync = torch.zeros(cfg.num_hidden_layers, words, dtype=torch.int32,
-                                          device=dev)
-            self.chain_err = torch.zeros(1, dtype=torch.int32, device=dev)
-            self.chains = [self._build_chain(i) for i in range(cfg.num_hidden_layers)]
 
     # ------------------------------------------------------------------ state
     def _reset_cache(self):
@@ -182,40 +164,6 @@ class Qwen35FP8Engine:
             return self.mix_out[:self.cfg.attn_out_dim], ly["o_proj"]
         return self.mix_out[:self.cfg.value_dim], ly["out_proj"]
 
-    def _chain_shapes_ok(self):
-        """qh_chain's fast-path shapes: hidden 2560, output-projection K 4096,
-        MLP 9216, fp32 128x128 block scales everywhere."""
-        cfg = self.cfg
-        if (cfg.hidden_size, cfg.intermediate_size) != (2560, 9216):
-            return False
-        for i in range(cfg.num_hidden_layers):
-            x, wo = self._out_proj(i)
-            mats = [wo, self.w.layers[i]["gate_proj"], self.w.layers[i]["up_proj"],
-                    self.w.layers[i]["down_proj"]] + [ws for ws, _ in self._in_segs(i)]
-            if x.numel() != 4096:
-                return False
-            for w, s in mats:
-                if s.dtype != torch.float32 or s.dim() != 2 or s.shape[1] * 128 != w.shape[1] \
-                        or s.shape[0] != (w.shape[0] + 127) // 128:
-                    return False
-        return True
-
-    def _build_chain(self, i):
-        """Phases of layer i's chain: output projection (+ residual h -> h2),
-        gate/up (h2 -> m), down (+ residual h2 -> h), then layer i+1's input
-        projection (h -> q/k/v or qkv/z/a/b) unless i is the last layer."""
-        ly = self.w.layers[i]
-        x, wo = self._out_proj(i)
-        ph = [ops.chain_gemv_phase(x, [(wo, self.h2)], res=self.h, eps=self.eps),
-              ops.chain_mlp_phase(self.h2, ly["post_attention_layernorm"], ly["gate_proj"],
-                                  ly["up_proj"], self.m, eps=self.eps),
-              ops.chain_gemv_phase(self.m, [(ly["down_proj"], self.h)], res=self.h2, eps=self.eps)]
-        if i + 1 < self.cfg.num_hidden_layers:
-            ph.append(ops.chain_gemv_phase(self.h, self._in_segs(i + 1),
-                                           norm_w=self.w.layers[i + 1]["input_layernorm"],
-                                           eps=self.eps))
-        return (abi.ChainPhase * len(ph))(*ph)
-
     def _split_gdn_ok(self):
         cfg = self.cfg
         if (cfg.linear_key_head_dim, cfg.linear_value_head_dim) != (128, 128) \
@@ -228,10 +176,6 @@ class Qwen35FP8Engine:
             if ops.scale_mode(w, s) != w.shape[1] // 128:
                 return False
         return True
-
-    def chain_error(self):
-        """True if a chained launch's bounded wait expired (results invalid)."""
-        return self.use_chain and int(self.chain_err.item()) != 0
 
     def _mixer(self, i):
         cfg, L, ly = self.cfg, self.lib, self.w.layers[i]
@@ -335,15 +279,9 @@ class Qwen35FP8Engine:
         self._pre(0)
         for i in range(n):
             self._mixer(i)
-            if self.use_chain:
-                arr = self.chains[i]
-                abi.check(self.lib.qh_chain(ctypes.cast(arr, ctypes.c_void_p), len(arr),
-                                            abi.ptr(self.chain_sync[i]), abi.ptr(self.chain_err),
-                                            abi.stream_handle()), "qh_chain")
-            else:
-                self._post(i)
-                if i + 1 < n:
-                    self._pre(i + 1)
+            self._post(i)
+            if i + 1 < n:
+                self._pre(i + 1)
         self._head()
         self._sample()
 

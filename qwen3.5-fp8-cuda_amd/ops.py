@@ -152,38 +152,3 @@ def rmsnorm(x, weight, eps=1e-6, out=None):
     abi.check(lib.qh_rmsnorm(abi.ptr(x), abi.ptr(weight), abi.ptr(dst), rows, D, eps,
                              abi.stream_handle()), "rmsnorm")
     return dst
-
-
-# ------------------------------------------------------------------ chains
-def chain_gemv_phase(x, segs, norm_w=None, res=None, eps=1e-6, nwg=0):
-    """A grouped-GEMV phase for qh_chain: segs = [((w, s), y), ...] (<= 4),
-    optional (1+w) RMSNorm weight on x and residual res added to the output."""
-    ph = abi.ChainPhase()
-    ph.kind, ph.nwg = abi.ChainPhase.GEMV, nwg
-    ph.x, ph.norm_w, ph.res1 = abi.ptr(x), abi.ptr(norm_w), abi.ptr(res)
-    ph.eps, ph.K, ph.nseg = eps, x.numel(), len(segs)
-    for i, ((w, s), y) in enumerate(segs):
-        ph.w[i], ph.s[i], ph.y[i] = abi.ptr(w), abi.ptr(s), abi.ptr(y)
-        ph.n[i], ph.kb[i] = w.shape[0], scale_mode(w, s)
-    return ph
-
-
-def chain_mlp_phase(x, norm_w, gate, up, m_out, eps=1e-6, nwg=0):
-    """A gate/up phase for qh_chain: m_out = bf16(silu(gate x) * (up x)) of the
-    (1+w)-normalised x."""
-    (wg, sg), (wu, su) = gate, up
-    ph = abi.ChainPhase()
-    ph.kind, ph.nwg = abi.ChainPhase.MLP, nwg
-    ph.x, ph.norm_w, ph.eps, ph.K = abi.ptr(x), abi.ptr(norm_w), eps, x.numel()
-    ph.w[0], ph.s[0], ph.w[1], ph.s[1] = abi.ptr(wg), abi.ptr(sg), abi.ptr(wu), abi.ptr(su)
-    ph.y[0], ph.n[0], ph.kb[0] = abi.ptr(m_out), wg.shape[0], scale_mode(wg, sg)
-    return ph
-
-
-def launch_chain(phases, sync, err=None):
-    """Launch up to 4 dependent phases on the current stream (qh_chain)."""
-    import ctypes
-    arr = (abi.ChainPhase * len(phases))(*phases)
-    lib = abi.load()
-    abi.check(lib.qh_chain(ctypes.cast(arr, ctypes.c_void_p), len(phases), abi.ptr(sync),
-                           abi.ptr(err), abi.stream_handle()), "qh_chain")

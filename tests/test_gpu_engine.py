@@ -67,43 +67,6 @@ def test_graph_replay_equals_eager():
     assert torch.equal(le, lg)
 
 
-def _wide(num_layers=4, vocab=4096):
-    """The 4B layer widths (hidden 2560, MLP 9216, 16x256 attention, 32x128
-    GatedDeltaNet) with fewer layers and a small vocabulary."""
-    import dataclasses
-    from qwen35_amd.config import qwen35_4b
-    return dataclasses.replace(qwen35_4b(), num_hidden_layers=num_layers, vocab_size=vocab,
-                               layer_types=None)
-
-
-@pytest.mark.parametrize("graph", [False, True])
-def test_chained_launches_equal_separate_launches(graph):
-    """The chained engine (out_proj/gate-up/down/next in_proj per launch, opt-in)
-    gives bit-identical logits and tokens to the engine launching each kernel
-    (with the same fused GatedDeltaNet step: split_gdn=False)."""
-    cfg = _wide()
-    w = make_weights(cfg, seed=3, device="cuda")
-    prompt = make_prompt(cfg, n=5, seed=4)
-    out = []
-    for chain in (True, False):
-        eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=64, use_chain=chain, split_gdn=False)
-        assert eng.use_chain == chain
-        if graph:
-            eng.capture()
-        eng._reset_cache()
-        eng.prefill(prompt.view(1, -1).cuda())
-        first = eng.logits.float().cpu().clone()
-        eng.generate(6)
-        torch.cuda.synchronize()
-        assert not eng.chain_error()
-        out.append((first, eng.tokens(4, 11).cpu().tolist(), eng.logits.float().cpu().clone()))
-        del eng
-    (f1, t1, l1), (f2, t2, l2) = out
-    assert torch.equal(f1, f2)
-    assert t1 == t2
-    assert torch.equal(l1, l2)
-
-
 def test_engine_on_loaded_checkpoint_bf16_scales(tmp_path):
     """A checkpoint written in the released layout, loaded like the reference
     loads it (scale_inv rounded to bf16), decodes like the oracle on the same
