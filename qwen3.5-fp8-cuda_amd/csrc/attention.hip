@@ -131,15 +131,23 @@ __device__ __forceinline__ void load_norm_w(NormRopeIn<NPL>& in, const float* q_
     in.kw[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rk, off, 0, 0));
   }
 }
+// cos / sin rows of the tables at the position.  Buffer loads over exactly the
+// row keep this branch-free (dims c >= rot read past the range: zeros, replaced
+// by cos 1, sin 0), so the loads can be issued ahead of the K/V tile and
+// waited for without waiting for the tile.
 template <int NPL>
 __device__ __forceinline__ void load_rope(NormRopeIn<NPL>& in, const float* cos_row, const float* sin_row,
                                           int rot, int lane) {
+  const int bytes = rot > 0 ? rot * 4 : 0;
+  const auto rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(cos_row), (short)0, bytes, 0x00020000);
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sin_row), (short)0, bytes, 0x00020000);
 #pragma unroll
   for (int i = 0; i < NPL; ++i) {
     const int c = lane * NPL + i;
-    const int cr = c < rot ? c : 0;
-    in.cs[i] = rot > 0 ? cos_row[cr] : 1.0f;
-    in.sn[i] = rot > 0 ? sin_row[cr] : 0.0f;
+    const float cv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rc, c * 4, 0, 0));
+    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, c * 4, 0, 0));
+    in.cs[i] = c < rot ? cv : 1.0f;
+    in.sn[i] = c < rot ? sv : 0.0f;
   }
 }
 
@@ -172,15 +180,15 @@ __device__ __forceinline__ void norm_rope(float (&v)[D / 64], bool has_norm, con
   }
 }
 
-template <int D>
+// HPW: query heads per wave, ceil(G / 4) for the GQA group size G.
+template <int D, int HPW>
 __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
   constexpr int NPL = D / 64;
   constexpr int KS = D + 16;  // padded K row (bf16): conflict-free 16-byte LDS reads
-  constexpr int HPW = MAXG / 4;
   __shared__ __align__(16) uint16_t sK[TP * KS];
   __shared__ __align__(16) uint16_t sV[TP * D];
   __shared__ __align__(16) uint16_t sQ[MAXG * D];
-  __shared__ float sP[MAXG][TP];
+  __shared__ __align__(16) float sP[MAXG][TP];
   __shared__ __align__(16) uint16_t sKn[D];
   __shared__ __align__(16) uint16_t sVn[D];
   __shared__ int s_last;
@@ -281,8 +289,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
       *(u32x4*)(sV + row * D + c8) = vq;
     }
   };
-  if (p0 < p1) fetch(p0, p1);
+  // cos / sin first: waiting for them (the norm and rotation below) then
+  // does not wait for the tile requested after them.  Every workgroup that
+  // gets here holds positions (p0 < p1: split 0 starts at 0 < total, the
+  // others returned above unless split < nactive), so the fetch needs no
+  // branch, which would make the compiler wait for all loads at the join.
   load_rope<NPL>(nr, cos_row, sin_row, p.rot, lane);
+  fetch(p0, p1);
 
   // ---- query heads of this KV group: norm + RoPE, kept as bf16 in LDS ----
 #pragma unroll
@@ -319,23 +332,35 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     for (int i = 0; i < NPL; ++i) o[hi][i] = 0.0f;
   }
 
+  // scores: lane pair (2j, 2j+1) owns position t0+j, each lane half the dims
+  // (chunks of 8 dims c = 2 cc + half); the lane's q chunks stay in registers
+  // for the whole loop, so only K is read from LDS per position.
+  const int prow = lane >> 1, half = lane & 1;
+  u32x4 qreg[HPW][D / 16];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi < G ? wid + 4 * hi : 0;
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) qreg[hi][cc] = *(const u32x4*)(sQ + gi * D + (2 * cc + half) * 8);
+  }
+
   for (int t0 = p0; t0 < p1; t0 += TP) {
     stage(t0);
     __syncthreads();
     if (t0 + TP < p1) fetch(t0 + TP, p1);
 
-    // scores: lane pair (2j, 2j+1) owns position t0+j, each lane half the dims
-    const int prow = lane >> 1, half = lane & 1;
     const bool valid = t0 + prow < p1;
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
       const int gi = wid + 4 * hi;
       if (gi < G) {
         float dot = 0.0f;
+        // constant trip count: unrolled, the LDS reads are issued together
 #pragma unroll
-        for (int c = half; c < D / 8; c += 2) {
+        for (int cc = 0; cc < D / 16; ++cc) {
+          const int c = 2 * cc + half;
           const u32x4 k8 = *(const u32x4*)(sK + prow * KS + c * 8);
-          const u32x4 q8 = *(const u32x4*)(sQ + gi * D + c * 8);
+          const u32x4 q8 = qreg[hi][cc];
           dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.x), as_bf2(k8.x), dot, false);
           dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.y), as_bf2(k8.y), dot, false);
           dot = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q8.z), as_bf2(k8.z), dot, false);
@@ -360,13 +385,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     for (int hi = 0; hi < HPW; ++hi) {
       const int gi = wid + 4 * hi;
       if (gi < G) {
-#pragma unroll 8
-        for (int j = 0; j < TP; ++j) {
-          const float pj = sP[gi][j];
-          float vv[NPL];
-          load_head<NPL>(vv, sV + j * D + lane * NPL);
+        // fully unrolled: the V reads and the 4-position p reads issue ahead
 #pragma unroll
-          for (int i = 0; i < NPL; ++i) o[hi][i] = fmaf(pj, vv[i], o[hi][i]);
+        for (int j4 = 0; j4 < TP / 4; ++j4) {
+          const float4 p4 = *(const float4*)&sP[gi][4 * j4];
+          const float pj[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float vv[NPL];
+            load_head<NPL>(vv, sV + (4 * j4 + u) * D + lane * NPL);
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) o[hi][i] = fmaf(pj[u], vv[i], o[hi][i]);
+          }
         }
       }
     }
@@ -421,7 +451,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
     const float ms = have ? pub_load(base + lane * sstride + D) : -INFINITY;
     // The partials of MB splits are requested together (one memory round trip
     // per batch, not per split; the first batch travels with the (m, l)
-    // loads); slots past the last active split load zeros.
+    // loads); slots past the last active split load zeros.  (A 16-wide batch
+    // above 8 active splits measured no faster.)
     constexpr int MB = 8;
     float part[MB][NPL];
 #pragma unroll
@@ -533,10 +564,14 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
     }
   }
   dim3 grid(p.n_kv, p.nsplit);
-  if (head_dim == 256)
-    hipLaunchKernelGGL(attn_decode_kernel<256>, grid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, p);
+  const bool two = p.n_heads / p.n_kv > 4;  // two query heads per wave
+  if (head_dim == 256) {
+    if (two) hipLaunchKernelGGL((attn_decode_kernel<256, 2>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<256, 1>), grid, dim3(256), 0, st, p);
+  } else {
+    if (two) hipLaunchKernelGGL((attn_decode_kernel<128, 2>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_decode_kernel<128, 1>), grid, dim3(256), 0, st, p);
+  }
   return 0;
 }
 

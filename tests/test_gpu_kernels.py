@@ -10,6 +10,7 @@ import torch
 
 from oracle import qwen35_oracle as orc
 from qwen35_amd import abi, ops
+from qwen35_amd import engine as eng_mod
 
 from _util import assert_close, bf, cos_sim, gen, quant, randn
 
@@ -256,7 +257,15 @@ def test_attn_decode(ctx, splits):
     g = gen(ctx)
     Hq, Hkv, D, rot, max_seq = 16, 4, 256, 64, 4096
     kc, vc, q_all, k_new, v_new, qn, kn = _attn_case(g, ctx, max_seq=max_seq)
-    cos, sin = orc.rope_tables(max_seq, rot, 1e7)
+    # Cache rows past the context hold NaN: no split may read a row it does
+    # not own into the result.
+    kc[:, ctx:] = float("nan")
+    vc[:, ctx:] = float("nan")
+    # Tables built on the device, as the reference builds them (main.py:527-533)
+    # and the engine does; the oracle reads the same values (host-built ones
+    # can differ in the last bit at large angles).
+    gcos, gsin = eng_mod.rope_tables(max_seq, rot, 1e7, device=DEV)
+    cos, sin = gcos.cpu(), gsin.cpu()
     pos = ctx - 1
     kc_ref, vc_ref = kc.clone(), vc.clone()
     ref = orc.attn_decode(q_all.float(), k_new.float(), v_new.float(), qn, kn, cos, sin, kc_ref,
@@ -270,13 +279,13 @@ def test_attn_decode(ctx, splits):
     qa = cu(q_all)
     for use_dev_pos in (True, False):
         abi.check(lib.qh_attn_decode(abi.ptr(qa), 2 * D, abi.ptr(qa[D:]), 2 * D, abi.ptr(cu(k_new)),
-                                     abi.ptr(cu(v_new)), abi.ptr(cu(qn)), abi.ptr(cu(kn)), abi.ptr(cu(cos)),
-                                     abi.ptr(cu(sin)), abi.ptr(kcg), abi.ptr(vcg), max_seq, D, rot, Hq, Hkv,
+                                     abi.ptr(cu(v_new)), abi.ptr(cu(qn)), abi.ptr(cu(kn)), abi.ptr(gcos),
+                                     abi.ptr(gsin), abi.ptr(kcg), abi.ptr(vcg), max_seq, D, rot, Hq, Hkv,
                                      abi.ptr(posd) if use_dev_pos else None, pos, splits,
                                      abi.ptr(scratch), abi.ptr(counters), abi.ptr(out), 1e-6,
                                      abi.stream_handle()))
         sync()
-        assert_close(out, ref, atol_frac=1e-3, what=f"attn ctx={ctx} splits={splits}")
+        assert_close(out, ref, atol_frac=1e-3, what=f"attn ctx={ctx} splits={splits} dev_pos={use_dev_pos}")
         assert torch.equal(kcg[:, pos].cpu().float(), kc_ref[:, pos]), "K cache slot"
         assert torch.equal(vcg[:, pos].cpu().float(), vc_ref[:, pos]), "V cache slot"
         assert int(counters.abs().sum()) == 0, "arrival counters must self-reset"
