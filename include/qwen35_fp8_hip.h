@@ -330,6 +330,18 @@ int qh_gdn_scan(const void* qn, const void* kn, const void* y, const float* g, c
                 const void* z, const void* norm_w, float* state, void* out, int M, int Hk, int Hv,
                 int dk, int dv, float eps, qh_stream_t stream);
 
+/* Workspace bytes of qh_gdn_chunk for M tokens and Hv value heads
+ * (Hv * ceil(M / 64) * 98560). */
+size_t qh_gdn_chunk_workspace_size(int M, int Hv);
+
+/* qh_gdn_scan in the chunked (WY) form the reference's prefill uses
+ * (main.py:1139-1149, transformers torch_chunk_gated_delta_rule, chunk 64)
+ * on the bf16 matrix cores: same operands and results (dk = dv = 128), plus a
+ * device workspace of qh_gdn_chunk_workspace_size(M, Hv) bytes. */
+int qh_gdn_chunk(const void* qn, const void* kn, const void* y, const float* g, const void* beta,
+                 const void* z, const void* norm_w, float* state, void* out, int M, int Hk, int Hv,
+                 int dk, int dv, float eps, void* ws, size_t ws_bytes, qh_stream_t stream);
+
 /* m = bf16(bf16(silu(g)) * u), the M > 1 MLP glue (replaces main.py:1213-1215). */
 int qh_silu_mul(const void* g, const void* u, void* m, size_t n, qh_stream_t stream);
 

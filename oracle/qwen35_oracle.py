@@ -274,12 +274,13 @@ def gated_delta_rule_seq(q, k, v, g, beta, S):
     return out
 
 
-def chunk_gated_delta_rule(q, k, v, g, beta, chunk=64):
-    """Chunked (WY) gated delta rule with zero initial state, restating the
-    algorithm transformers implements in torch_chunk_gated_delta_rule
-    (modeling_qwen3_5.py:249-328): within a chunk, the triangular system
-    (I + tril(diag(beta) K K^T * decay)) is solved by forward substitution;
-    chunks are chained through the state.  Inputs as gated_delta_rule_seq.
+def chunk_gated_delta_rule(q, k, v, g, beta, chunk=64, S0=None):
+    """Chunked (WY) gated delta rule, restating the algorithm transformers
+    implements in torch_chunk_gated_delta_rule (modeling_qwen3_5.py:249-328):
+    within a chunk, the triangular system (I + tril(diag(beta) K K^T * decay))
+    is solved by forward substitution; chunks are chained through the state,
+    which starts at S0 [H, dk, dv] (the reference's initial_state, main.py:1130,
+    passed when past_len > 0) or zero.  Inputs as gated_delta_rule_seq.
     Returns (o [T, H, dv], S [H, dk, dv])."""
     T, H, dk = k.shape
     dv = v.shape[-1]
@@ -288,7 +289,7 @@ def chunk_gated_delta_rule(q, k, v, g, beta, chunk=64):
         return torch.cat([x, torch.zeros(pad, *x.shape[1:])], 0) if pad else x
     q, k, v, g, beta = P(q), P(k), P(v), P(g), P(beta)
     n = (T + pad) // chunk
-    S = torch.zeros(H, dk, dv)
+    S = torch.zeros(H, dk, dv) if S0 is None else S0.clone().float()
     out = torch.zeros(T + pad, H, dv)
     for c in range(n):
         sl = slice(c * chunk, (c + 1) * chunk)

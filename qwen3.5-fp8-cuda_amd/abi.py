@@ -89,6 +89,8 @@ NATIVE_SIGNATURES = {
     "qh_attn_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp] + [_i] * 6 + [_vp]),
     "qh_gdn_prep": (_i, [_vp] * 12 + [_i] * 6 + [_vp]),
     "qh_gdn_scan": (_i, [_vp] * 9 + [_i] * 5 + [_f, _vp]),
+    "qh_gdn_chunk_workspace_size": (_sz, [_i, _i]),
+    "qh_gdn_chunk": (_i, [_vp] * 9 + [_i] * 5 + [_f, _vp, _sz, _vp]),
     "qh_silu_mul": (_i, [_vp, _vp, _vp, _sz, _vp]),
 }
 

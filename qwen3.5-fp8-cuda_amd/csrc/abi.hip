@@ -811,6 +811,23 @@ QH_EXPORT int qh_gdn_scan(const void* qn, const void* kn, const void* y, const f
   return check_launch("qh_gdn_scan");
 }
 
+// Workspace bytes of qh_gdn_chunk for M tokens and Hv value heads.
+QH_EXPORT size_t qh_gdn_chunk_workspace_size(int M, int Hv) { return qh_gdn_chunk_ws_bytes(M, Hv); }
+
+// qh_gdn_scan in the chunked (WY) form of torch_chunk_gated_delta_rule, the
+// reference's prefill algorithm (main.py:1139-1149), on the matrix cores:
+// same operands and results, plus a workspace of qh_gdn_chunk_workspace_size.
+QH_EXPORT int qh_gdn_chunk(const void* qn, const void* kn, const void* y, const float* g,
+                           const void* beta, const void* z, const void* norm_w, float* state,
+                           void* out, int M, int Hk, int Hv, int dk, int dv, float eps, void* ws,
+                           size_t ws_bytes, hipStream_t stream) {
+  QhGdnScanParams p = {(const uint16_t*)qn, (const uint16_t*)kn, (const uint16_t*)y, g,
+                       (const uint16_t*)beta, (const uint16_t*)z, (const uint16_t*)norm_w, state,
+                       (uint16_t*)out, M, 2 * Hk * dk + Hv * dv, Hk, Hv, dk, dv, eps};
+  if (qh_launch_gdn_chunk(p, (float*)ws, ws_bytes, stream) != 0) return -1;
+  return check_launch("qh_gdn_chunk");
+}
+
 // m = bf16(bf16(silu(g)) * u), the M > 1 MLP glue (main.py:1213-1215).
 QH_EXPORT int qh_silu_mul(const void* g, const void* u, void* m, size_t n, hipStream_t stream) {
   if (qh_launch_silu_mul((const uint16_t*)g, (const uint16_t*)u, (uint16_t*)m, n, stream) != 0)

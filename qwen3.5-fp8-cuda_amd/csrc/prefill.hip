@@ -421,6 +421,11 @@ int qh_launch_gdn_scan(const QhGdnScanParams& p, hipStream_t st) {
   // 4 columns per wave (1024 waves at Hv = 32): 128-token prompt 10.32 ms vs
   // 10.44 ms with 8 columns per wave
   hipLaunchKernelGGL(gdn_scan_kernel<4>, dim3(p.Hv * (128 / 4)), dim3(64), 0, st, p);
+  return qh_launch_gdn_gated_norm(p, st);
+}
+
+int qh_launch_gdn_gated_norm(const QhGdnScanParams& p, hipStream_t st) {
+  if (p.M <= 0) return 0;
   hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(p.M, p.Hv), dim3(128), 0, st, p);
   return 0;
 }

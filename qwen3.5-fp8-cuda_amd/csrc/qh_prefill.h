@@ -73,5 +73,11 @@ int qh_launch_attn_prep(const QhAttnPrepParams& p, hipStream_t st);
 int qh_launch_attn_prefill(const QhAttnPrefillParams& p, hipStream_t st);
 int qh_launch_gdn_prep(const QhGdnPrepParams& p, hipStream_t st);
 int qh_launch_gdn_scan(const QhGdnScanParams& p, hipStream_t st);
+// gated RMSNorm of the bf16 core in p.out, in place (gdn_gated_norm_kernel)
+int qh_launch_gdn_gated_norm(const QhGdnScanParams& p, hipStream_t st);
+// Chunked (WY) form of qh_launch_gdn_scan on the matrix cores (gdn_chunk.hip);
+// ws: qh_gdn_chunk_ws_bytes(M, Hv) bytes, 16-byte aligned.
+size_t qh_gdn_chunk_ws_bytes(int M, int Hv);
+int qh_launch_gdn_chunk(const QhGdnScanParams& p, float* ws, size_t ws_bytes, hipStream_t st);
 int qh_launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* m, size_t n, hipStream_t st);
 void qh_set_error(const char* fmt, ...);

@@ -84,6 +84,18 @@ def test_validation_errors_need_no_gpu():
     rc = lib.qh_gdn_decode(None, None, None, None, None, None, None, None, None, None, None, None, None,
                            None, 0, 16, 32, 64, 128, 1e-6, None)
     assert rc == -1 and "dk" in abi.last_error()
+    # chunked GatedDeltaNet prefill: shape and workspace checks before any launch
+    rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 64, 16, 32, 64, 128,
+                          1e-6, None, 0, None)
+    assert rc == -1 and "unsupported shape" in abi.last_error()
+    need = int(lib.qh_gdn_chunk_workspace_size(130, 32))
+    assert need == 32 * 3 * 98560
+    rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, 16, 32, 128, 128,
+                          1e-6, None, need, None)
+    assert rc == -1 and "workspace" in abi.last_error()
+    rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, 16, 32, 128, 128,
+                          1e-6, ctypes.c_void_p(256), need - 1, None)
+    assert rc == -1 and "workspace" in abi.last_error()
     rc = lib.qh_gemm_e4m3(None, None, None, None, 4, 4, 100, 1, 0, None, None)
     assert rc == -1
     # grouped GEMM: every check runs before anything touches a device pointer

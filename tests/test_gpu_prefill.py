@@ -70,8 +70,13 @@ def test_attention_prefill(M, past_fill):
 # M = 45: five full 8-token blocks of the scan plus a tail; M = 3: fewer
 # tokens than the conv window (the ring supplies them all); past > 0 with a
 # filled ring and state: the conv reads positions before the prompt.
-@pytest.mark.parametrize("M,past", [(45, 0), (3, 0), (8, 6), (21, 6)])
-def test_gdn_prefill(M, past):
+# algo "chunk" (qh_gdn_chunk): M = 64 one full chunk, 130 two chunks and a
+# 2-token tail, 200 from a stored state over four chunks.
+@pytest.mark.parametrize("M,past,algo", [(45, 0, "scan"), (3, 0, "scan"), (8, 6, "scan"),
+                                         (21, 6, "scan"), (45, 0, "chunk"), (3, 0, "chunk"),
+                                         (21, 6, "chunk"), (64, 0, "chunk"), (130, 0, "chunk"),
+                                         (200, 6, "chunk")])
+def test_gdn_prefill(M, past, algo):
     g = gen(22 + M + past)
     Hk, Hv, dk, dv = 2, 4, 128, 128
     C = 2 * Hk * dk + Hv * dv
@@ -99,9 +104,17 @@ def test_gdn_prefill(M, past):
     abi.check(lib.qh_gdn_prep(abi.ptr(dm), abi.ptr(ring), abi.ptr(dw), abi.ptr(da), abi.ptr(db),
                               abi.ptr(dA), abi.ptr(ddt), abi.ptr(y), abi.ptr(qn), abi.ptr(kn),
                               abi.ptr(gg), abi.ptr(beta), M, Hk, Hv, dk, dv, past, st))
-    abi.check(lib.qh_gdn_scan(abi.ptr(qn), abi.ptr(kn), abi.ptr(y), abi.ptr(gg), abi.ptr(beta),
-                              abi.ptr(dz), abi.ptr(dnw), abi.ptr(state), abi.ptr(out), M, Hk, Hv,
-                              dk, dv, 1e-6, st))
+    if algo == "scan":
+        abi.check(lib.qh_gdn_scan(abi.ptr(qn), abi.ptr(kn), abi.ptr(y), abi.ptr(gg), abi.ptr(beta),
+                                  abi.ptr(dz), abi.ptr(dnw), abi.ptr(state), abi.ptr(out), M, Hk, Hv,
+                                  dk, dv, 1e-6, st))
+    else:
+        nws = int(lib.qh_gdn_chunk_workspace_size(M, Hv))
+        assert nws == Hv * ((M + 63) // 64) * 98560
+        ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+        abi.check(lib.qh_gdn_chunk(abi.ptr(qn), abi.ptr(kn), abi.ptr(y), abi.ptr(gg), abi.ptr(beta),
+                                   abi.ptr(dz), abi.ptr(dnw), abi.ptr(state), abi.ptr(out), M, Hk, Hv,
+                                   dk, dv, 1e-6, abi.ptr(ws), nws, st))
     torch.cuda.synchronize()
     # oracle: OracleModel._gdn_prefill after the projections
     # window history: slot (past - 3 + i) % 4 of the ring holds position past - 3 + i
@@ -133,6 +146,14 @@ def test_gdn_prefill(M, past):
     gated = orc.gated_rmsnorm(orc.bf16(o), z.float().view(M, Hv, dv), norm_w, 1e-6, bf16_steps=True)
     assert_close(out.view(M, Hv, dv), gated, atol_frac=1e-3, what="gated output")
     assert_close(state, S, rtol=1e-3, atol_frac=1e-4, what="final state")
+    if algo == "chunk":
+        # the reference's own (chunked) algorithm from the same state
+        o_c, S_c = orc.chunk_gated_delta_rule(qh * (1.0 / math.sqrt(dk)), kh, vh, gg.cpu(),
+                                              beta.cpu().float(), S0=state0)
+        gated_c = orc.gated_rmsnorm(orc.bf16(o_c), z.float().view(M, Hv, dv), norm_w, 1e-6,
+                                    bf16_steps=True)
+        assert_close(out.view(M, Hv, dv), gated_c, atol_frac=1e-3, what="gated output (chunked)")
+        assert_close(state, S_c, rtol=1e-3, atol_frac=1e-4, what="final state (chunked)")
 
 
 def test_silu_mul_exact():
@@ -146,6 +167,26 @@ def test_silu_mul_exact():
     torch.cuda.synchronize()
     ref = orc.bf16(orc.bf16(F.silu(a.float())) * b.float())
     assert torch.equal(out.cpu().float(), ref)
+
+
+def test_engine_batch_prefill_chunked_gdn_matches_oracle():
+    """A 150-token prompt: the engine's GatedDeltaNet layers take the chunked
+    (WY) matrix-core path (qh_gdn_chunk); logits against the oracle's reference
+    prefill (recurrent rule), then a second batch prefill continuing at
+    past_len 150 from the stored state."""
+    cfg = tiny(num_layers=4)
+    w = make_weights(cfg, seed=0)
+    prompt = make_prompt(cfg, n=150, seed=3)
+    more = make_prompt(cfg, n=100, seed=4)
+    assert prompt.numel() >= eng_mod.GDN_CHUNK_MIN_TOKENS and more.numel() >= eng_mod.GDN_CHUNK_MIN_TOKENS
+    eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=256)
+    ref = orc.OracleModel(w, max_seq_len=256, prefill="reference")
+    l1 = eng.forward(prompt.view(1, -1).cuda(), 0).float().cpu().view(-1)
+    r1 = ref.forward(prompt.view(1, -1), 0).view(-1)
+    assert cos_sim(l1, r1) > 0.9999
+    l2 = eng.forward(more.view(1, -1).cuda(), 150).float().cpu().view(-1)
+    r2 = ref.forward(more.view(1, -1), 150).view(-1)
+    assert cos_sim(l2, r2) > 0.9999
 
 
 def test_engine_batch_prefill_matches_oracle_reference_prefill():

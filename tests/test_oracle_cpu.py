@@ -189,6 +189,27 @@ def test_recurrent_equals_chunked_rule():
     assert torch.allclose(S, S_chk, rtol=1e-4, atol=1e-4)
 
 
+def test_chunked_rule_from_initial_state_equals_recurrent():
+    """The initial-state path of the chunked rule (prefill at past_len > 0)
+    against the recurrence from the same state, over 2.5 chunks."""
+    g = gen(19)
+    T, H, dk, dv = 160, 2, 32, 24
+    q = F.normalize(randn(g, T, H, dk), dim=-1) / math.sqrt(dk)
+    k = F.normalize(randn(g, T, H, dk), dim=-1)
+    v = randn(g, T, H, dv)
+    gl = -torch.rand(T, H, generator=g) * 0.5
+    beta = torch.sigmoid(randn(g, T, H))
+    S0 = randn(g, H, dk, dv, std=0.3)
+    S = S0.clone()
+    o_rec = orc.gated_delta_rule_seq(q, k, v, gl, beta, S)
+    o_chk, S_chk = orc.chunk_gated_delta_rule(q, k, v, gl, beta, S0=S0)
+    assert torch.allclose(o_rec, o_chk, rtol=1e-4, atol=1e-4)
+    assert torch.allclose(S, S_chk, rtol=1e-4, atol=1e-4)
+    # a wrong initial state is detected: zero start differs
+    o_zero, _ = orc.chunk_gated_delta_rule(q, k, v, gl, beta)
+    assert (o_zero - o_rec).abs().max() > 1e-2
+
+
 def test_l2norm_bf16_and_gates():
     g = gen(10)
     x = bf(randn(g, 5, 128)).float()
