@@ -139,7 +139,7 @@ def traffic_probe(eng, reps=2, copy_mib=256):
                       "copies": 4}))
 
 
-FP8_MFMA_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 matrix-core peak
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak (the GEMM's instruction)
 
 
 def prefill_gemm_inputs(seed=0):
@@ -208,13 +208,13 @@ def time_prefill_gemm(reps=20):
         us = a.elapsed_time(b) * 1e3 / reps
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
         res.append({"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
-                    "frac_fp8_dense_peak": round(tf / FP8_MFMA_PEAK_TFLOPS, 4)})
+                    "frac_bf16_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)})
     return {"config": "BASELINE configs[2]: X[512x2560] x W[9216x2560]^T and X'[512x9216] x "
                       "W'[2560x9216]^T, E4M3 128x128 block scales, seed 0",
-            "kernel": "gemm_e4m3_lds_kernel (v_mfma_scale_f32_32x32x64_f8f6f4; the bf16 activation "
-                      "split in-tile into hi+lo E4M3 terms with per-(row, 32-K) E8M0 run scales: "
-                      "two fp8 products per multiply-add, no workspace)",
-            "peak_tflops": FP8_MFMA_PEAK_TFLOPS, "gemms": res}
+            "kernel": "gemm_e4m3_lds_kernel (v_mfma_f32_32x32x16_bf16: E4M3 weights widened exactly "
+                      "to bf16 as they leave LDS, bf16 activations as is, fp32 products and "
+                      "accumulation; no workspace)",
+            "peak_tflops": BF16_MFMA_PEAK_TFLOPS, "gemms": res}
 
 
 def _graph_us(launches, reps=10):
@@ -436,6 +436,28 @@ def kernel_configs(eng, cpu=True):
     return res
 
 
+def launch_floor():
+    """Fixed cost of one kernel in a HIP graph on this box: the per-launch
+    period of 64 back-to-back launches of (a) torch's fill of a one-element
+    tensor (no memory traffic to speak of: the graph's launch floor) and
+    (b) the E4M3 GEMV on a 128 x 2560 weight (330 KB, resident in the MALL:
+    the floor plus one load-to-store round trip through the GEMV)."""
+    from qwen35_amd import abi, ops, synth
+    L = abi.load()
+    t1 = torch.zeros(1, device="cuda")
+    empty_us = _graph_us([lambda: t1.fill_(1.0)] * 64, reps=20)
+    g = torch.Generator().manual_seed(0)
+    w, s = (t.to("cuda") for t in synth.quantize_block_fp8(torch.randn(128, 2560, generator=g) * 0.02))
+    x = torch.randn(2560, generator=g).to(torch.bfloat16).to("cuda")
+    y = torch.empty(128, dtype=torch.bfloat16, device="cuda")
+    gemv = lambda: abi.check(L.qh_gemv_e4m3(
+        abi.ptr(x), None, None, 1e-6, 2560, None, None, 1, abi.ptr(w), abi.ptr(s), abi.ptr(y), 128,
+        ops.scale_mode(w, s), *([None, None, None, 0, 0] * 3), 0, abi.stream_handle()), "gemv")
+    gemv_us = _graph_us([gemv] * 64, reps=20)
+    return {"empty_kernel_us": round(empty_us, 3), "gemv_128x2560_us": round(gemv_us, 3),
+            "timing": "HIP graph of 64 launches replayed 20 times between HIP events"}
+
+
 def host_cpu():
     """The host's CPU as lscpu reports it (model, sockets, physical cores)."""
     info = {"os_cpu_count": os.cpu_count()}
@@ -645,6 +667,9 @@ def main():
     ctx0 = args.prompt + args.warmup
     bytes_tok = w.nbytes_per_token()
 
+    floor = launch_floor()
+    log(f"launch floor: {floor['empty_kernel_us']} us empty kernel, {floor['gemv_128x2560_us']} us "
+        f"128x2560 GEMV")
     mlp_us, n_launch = time_mlp_launches(eng)
     log(f"gate/up kernel: {mlp_us:.2f} us per launch")
     mbytes = mlp_bytes(cfg)
@@ -711,6 +736,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "memory": mem,
+        "launch_floor": floor,
         "prefill": prefill,
         "prefill_gemm": gemm,
         "kernels": kernels,
