@@ -11,19 +11,22 @@
 // multiply does, for any activation range.  Each 128-wide K block's fp32
 // partial is multiplied by the weight block scale and added to the fp32
 // accumulator.  The weights stream from HBM as one byte each; the widening
-// (two conversions per two weights) is repeated only by the M / 64 row tiles
-// that share a weight tile, and costs half the matrix-core time of its block.
+// (one conversion instruction per two weights) is repeated only by the M / 64
+// row tiles that share a weight tile.
 //
 // Nothing is precomputed and no workspace is needed; a caller workspace only
 // enables split-K (qh_gemm_e4m3 / qh_gemm_e4m3_grouped).  The reference entry
 // point fp8_gemm_batch passes none and never splits.
 //
-// Tiling: 64 x BN output tile per 256-thread workgroup (the launchers use
-// BN = 64), a 2 x 2 grid of waves each holding 32 x (BN/2) as BN/64 32x32
-// matrix-core tiles; tiles are ordered so that the row tiles of one weight
-// tile run on one XCD (see the kernel).  Each 128-wide K block of X (bf16, rows padded to 272 bytes) and W
-// (E4M3, rows padded to 144 bytes) is staged once per workgroup in LDS (two
-// stages), the next block in registers while the current one is multiplied.
+// Two kernels, both on 64 x 64 output tiles (a 2 x 2 grid of waves, each one
+// 32x32 matrix-core tile) in an XCD-aware tile order (the row tiles of one
+// weight tile run on one XCD and share it in that XCD's L2):
+//  - gemm_dma_kernel (every unsplit launch): persistent workgroups, three per
+//    CU, stream (tile, K block) units through a two-stage LDS ring filled by
+//    direct-to-LDS loads;
+//  - gemm_e4m3_lds_kernel (split-K): one workgroup per (tile, K slice), the
+//    next K blocks in registers while the current one is multiplied, fp32
+//    partials finished by gemm_splitk_reduce_kernel.
 // Operand layout of the 32x32x16 bf16 instruction (measured on gfx950):
 // lane l holds A[l % 32][8 (l / 32) + r] and B[8 (l / 32) + r][l % 32],
 // r = 0..7, and accumulator value e is C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
@@ -38,12 +41,16 @@ constexpr int kARow = 272;                      // padded LDS row of the X tile 
 constexpr int kBRow = 144;                      // padded LDS row of the W tile (bytes)
 constexpr int kBM = 64;                         // output rows per tile
 
-// Eight E4M3 weights (two words) widened to bf16, exactly.
+// Eight E4M3 weights (two words) widened to bf16, exactly: the scaled
+// conversion with scale 1 turns two codes into two bf16 in one instruction
+// (every finite E4M3 value, subnormals included, is a bf16 value; checked
+// bit for bit against the fp32 route for all 256 codes).
 __device__ __forceinline__ v8bf e4m3x8_bf16(u32x2 w) {
-  const auto a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
-  const auto c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
-  return v8bf{(__bf16)a[0], (__bf16)a[1], (__bf16)b[0], (__bf16)b[1],
-              (__bf16)c[0], (__bf16)c[1], (__bf16)d[0], (__bf16)d[1]};
+  const qh_bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.0f, false);
+  const qh_bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.0f, true);
+  const qh_bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.0f, false);
+  const qh_bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.0f, true);
+  return v8bf{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 // LDS of one K-block stage of a 64 x BN tile: X (64 rows), W (BN rows), the
@@ -61,6 +68,7 @@ struct GemmGroup {
   int N[4];
   int kb[4];
   int tstart[4];
+  int sbytes[4];    // scale array bytes, rounded up to whole words (persistent kernel)
   int nseg;
 };
 
@@ -226,6 +234,256 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint16_t* x, G
   }
 }
 
+// ---- persistent LDS-ring variant ----------------------------------------------
+// Persistent 256-thread workgroups (WPC per CU) walk their 64 x 64 output tiles
+// (XCD-aware order, as above) as one stream of (tile, 128-wide K block) units.
+// Each unit's X rows, W rows and per-column weight scales go straight from
+// memory to an LDS stage (buffer_load ... lds through range-checked buffer
+// resources based at the tile: rows past M or N read zeros), DS - 1 units
+// ahead, so the loads in flight cost no registers and the stream does not
+// drain between tiles.  16-byte slots are XOR-swizzled by row instead of padded
+// (the loads fill whole 1 KB runs): X row r (256 B) keeps chunk c in slot
+// c ^ (r % 16), so the 16-byte reads of 16 consecutive rows cover all 64
+// banks; W row r (128 B) keeps it in slot c ^ ((r / 2) % 8), which spreads
+// the 8-byte reads of 32 rows over the banks two to one.  Operands are read with
+// inline-asm LDS reads, which the compiler does not track (it would otherwise
+// wait for every outstanding ring load before each LDS read): each wave waits
+// for its own loads of the unit (vmcnt), all waves meet at a barrier, and each
+// matrix-core step waits only for its own two operand reads.
+constexpr int kDA = 64 * 256;                 // X rows of a unit: 64 x 128 bf16
+constexpr int kDB = 64 * 128;                 // W rows: 64 x 128 E4M3
+constexpr int kDSc = 4 * 256;                 // scales: one 64-word copy per wave
+constexpr int kDStage = kDA + kDB + kDSc;     // 25,600 B
+constexpr int kDLoads = 7;                    // loads per wave and unit: 4 X + 2 W + 1 scale
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ u32x4 ds_read16(uint32_t a) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x2 ds_read8(uint32_t a) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t ds_read4(uint32_t a) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+// Wait until at most N LDS reads are outstanding; a and b (the reads this
+// wait completes) are tied to it so that no use moves above it.
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x2& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+
+// One tile of the walk and its segment, all workgroup-uniform.
+struct DmaTile {
+  int tn, tm, nb, N, kb_code, sbytes;
+  const uint8_t* w;
+  const void* s;
+  uint16_t* y;
+};
+
+// The group is indexed in place (a kernel argument: scalar loads), never
+// copied to a local array.
+__device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m) {
+  DmaTile d;
+  d.tn = xc + 8 * (i / tiles_m);
+  d.tm = i % tiles_m;
+  int si = 0;
+#pragma unroll
+  for (int t = 1; t < 4; ++t)
+    if (t < g.nseg && d.tn >= g.tstart[t]) si = t;
+  d.w = g.w[si];
+  d.s = g.s[si];
+  d.y = g.y[si];
+  d.N = g.N[si];
+  d.kb_code = g.kb[si];
+  d.sbytes = g.sbytes[si];
+  d.nb = (d.tn - g.tstart[si]) * 64;
+  return d;
+}
+
+template <typename ScaleT, int DS>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGroup g, int M, int K,
+                                                       int tiles_n, int tiles_m) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int wm = (wid >> 1) * 32, wn = (wid & 1) * 32;
+  const int KB = K / 128;
+  // this workgroup's tiles: XCD xc, its j-th of P workgroups there; XCD xc
+  // owns N tiles xc, xc + 8, ... with all their row tiles (row tile fastest),
+  // dealt round-robin to its workgroups
+  const int xc = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3, P = (int)gridDim.x >> 3;
+  const int ntx = tiles_n > xc ? tiles_m * ((tiles_n - xc + 7) / 8) : 0;
+  const int my_tiles = j < ntx ? (ntx - j + P - 1) / P : 0;
+  const int U = my_tiles * KB;
+  if (U == 0) return;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)smem;
+
+  // lane-constant parts of the load offsets (the unit's K block is added)
+  uint32_t xo[4], wo[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // X: rows 16 wid + 4 i + lane / 16
+    const int row = 16 * wid + 4 * i + (lane >> 4);
+    xo[i] = ((uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 15) ^ (row & 15)) * 8)) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // W: rows 16 wid + 8 i + lane / 8
+    const int row = 16 * wid + 8 * i + (lane >> 3);
+    wo[i] = (uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) * 16);
+  }
+
+  // issue cursor: the unit whose loads go out next (it stays on the last unit
+  // once reached, so the ring keeps DS - 1 units of loads outstanding)
+  int it = 0, ikb = 0;
+  DmaTile itile = dma_tile(g, xc, j, tiles_m);
+  rsrc_t rx, rw, rs;
+  auto bind = [&]() {
+    const int rows_m = min(M - itile.tm * 64, 64), rows_n = min(itile.N - itile.nb, 64);
+    rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x + (size_t)itile.tm * 64 * K), (short)0,
+                                           rows_m * K * 2, 0x00020000);
+    rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(itile.w + (size_t)itile.nb * K), (short)0,
+                                           rows_n * K, 0x00020000);
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(itile.s), (short)0, itile.sbytes, 0x00020000);
+  };
+  bind();
+  auto issue = [&](int st) {
+    uint8_t* stage = smem + st * kDStage;
+    const uint32_t ko = (uint32_t)ikb * 256u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + (16 * wid + 4 * i) * 256), 16, xo[i] + ko,
+                                               0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + kDA + (16 * wid + 8 * i) * 128), 16,
+                                               wo[i] + (ko >> 1), 0, 0, 0);
+    // scales of this wave's 32 columns (lanes 32-63 repeat them), as the
+    // aligned words holding them
+    const int si = scale_index(itile.kb_code, min(itile.nb + wn + r, itile.N - 1), ikb);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + kDA + kDB + wid * 256), 4,
+                                             ((uint32_t)si * (uint32_t)sizeof(ScaleT)) & ~3u, 0, 0, 0);
+  };
+  auto advance = [&]() {
+    if (ikb + 1 < KB) {
+      ++ikb;
+    } else if (it + 1 < my_tiles) {
+      ++it;
+      ikb = 0;
+      itile = dma_tile(g, xc, j + it * P, tiles_m);
+      bind();
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < DS - 1; ++s) {
+    issue(s);
+    advance();
+  }
+
+  // compute cursor
+  int ckb = 0, ct = 0;
+  DmaTile ctile = dma_tile(g, xc, j, tiles_m);
+  v16f acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  const int arow = wm + r, brow = wn + r;
+  int st = 0;
+  for (int u = 0; u < U; ++u) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDLoads * (DS - 2)) : "memory");
+    __builtin_amdgcn_s_barrier();
+    issue(st == 0 ? DS - 1 : st - 1);
+    advance();
+    const uint32_t sa = lds0 + st * kDStage, sbb = sa + kDA;
+    u32x4 av[8];
+    u32x2 bv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      av[kk] = ds_read16(sa + arow * 256 + (((2 * kk + h) ^ (arow & 15)) << 4));
+      bv[kk] = ds_read8(sbb + brow * 128 + ((kk ^ ((brow >> 1) & 7)) << 4) + 8 * h);
+    }
+    uint32_t sw = ds_read4(sbb + kDB + wid * 256 + r * 4);
+    v16f t;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) t[e] = 0.0f;
+    // each step waits only for its own two operand reads
+#define QH_DMA_STEP(kk)                                                                   \
+  lds_wait<15 - 2 * (kk)>(av[kk], bv[kk]);                                                \
+  t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),          \
+                                              e4m3x8_bf16(bv[kk]), t, 0, 0, 0);           \
+  __builtin_amdgcn_sched_barrier(0);
+    QH_DMA_STEP(0) QH_DMA_STEP(1) QH_DMA_STEP(2) QH_DMA_STEP(3)
+    QH_DMA_STEP(4) QH_DMA_STEP(5) QH_DMA_STEP(6) QH_DMA_STEP(7)
+#undef QH_DMA_STEP
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw) : : "memory");
+    float scale;
+    if constexpr (sizeof(ScaleT) == 4) {
+      scale = __uint_as_float(sw);
+    } else {
+      const int idx = scale_index(ctile.kb_code, min(ctile.nb + wn + r, ctile.N - 1), ckb);
+      scale = (idx & 1) ? bf_hi(sw) : bf_lo(sw);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = fmaf(t[e], scale, acc[e]);
+    if (++ckb == KB) {  // the tile is complete: store it, start the next one
+      const int n = ctile.nb + wn + r;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[e]);
+        acc[e] = 0.0f;
+      }
+      ckb = 0;
+      if (++ct < my_tiles) ctile = dma_tile(g, xc, j + ct * P, tiles_m);
+    }
+    st = st == DS - 1 ? 0 : st + 1;
+  }
+  // no load may still be writing this workgroup's LDS when it exits
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Shape limit of the persistent kernel: its per-tile buffer ranges (64 rows
+// of K bf16) stay below 2^31 bytes.
+inline bool gemm_dma_fits(int K) { return (long)64 * K * 2 < 0x7fffffffL; }
+
+template <typename ScaleT, int DS>
+void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, hipStream_t st,
+                     int cus, int wpc) {
+  GemmGroup g = {};
+  g.nseg = nseg;
+  int tiles_n = 0;
+  for (int t = 0; t < nseg; ++t) {
+    g.w[t] = (const uint8_t*)seg[t].w;
+    g.s[t] = seg[t].s;
+    g.y[t] = (uint16_t*)seg[t].y;
+    g.N[t] = seg[t].N;
+    g.kb[t] = seg[t].kb;
+    g.tstart[t] = tiles_n;
+    tiles_n += (seg[t].N + 63) / 64;
+    const long n_scales = seg[t].kb > 1 ? (long)((seg[t].N + 127) / 128) * seg[t].kb
+                          : seg[t].kb == 1 ? seg[t].N : (long)seg[t].N * (-seg[t].kb);
+    // whole words: a 2-byte scale is read as the aligned word holding it
+    g.sbytes[t] = (int)min((n_scales * (long)sizeof(ScaleT) + 3) & ~3L, 0x7fffffffL);
+  }
+  const int tiles_m = (M + 63) / 64;
+  // P workgroups per XCD: as many as the busiest XCD has tiles (XCD 0 owns
+  // ceil(tiles_n / 8) N tiles), at most wpc per CU, so no workgroup there
+  // takes a second tile while others are idle
+  const long busiest = (long)tiles_m * ((tiles_n + 7) / 8);
+  const int P = (int)max(1L, min((long)cus * wpc / 8, busiest));
+  const int G = 8 * P;
+  hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g, M, K,
+                     tiles_n, tiles_m);
+}
+
 // Split-K finish: y = bf16(sum_z part[z][m][column]), summed in z order;
 // columns past a segment's N (tile padding) are skipped.  Four columns per
 // thread (segments start at multiples of 64 columns).
@@ -342,8 +600,8 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
   // 64x64 tiles: with the activation used as is, wider tiles only cut
-  // occupancy (64 x 128 measured 59.7 us against 48.8 us for config 3a's
-  // 512 x 9216 x 2560).
+  // occupancy or (weights loaded straight into operand registers) the load
+  // path's coalescing.
   const long tiles = tiles64 * mt;
   // Split-K (caller workspace only) when there are no more tiles than CUs:
   // the largest S <= 8 dividing the K blocks with >= 4 blocks per slice and
@@ -356,6 +614,17 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
       S = c;
       break;
     }
+  // Unsplit: the persistent ring kernel, three workgroups per CU (two 25 KB
+  // stages each), when its direct-to-LDS loads can take the operands as they
+  // are (16-byte aligned weights, word-aligned scales, tile ranges < 2 GiB).
+  bool ring = S == 1 && gemm_dma_fits(K);
+  for (int t = 0; t < nseg; ++t)
+    ring = ring && (uintptr_t)seg[t].w % 16 == 0 && (uintptr_t)seg[t].s % 4 == 0;
+  if (ring) {
+    if (scale_bf16) launch_gemm_dma<uint16_t, 2>(xa, seg, nseg, M, K, st, cus, 3);
+    else launch_gemm_dma<float, 2>(xa, seg, nseg, M, K, st, cus, 3);
+    return 0;
+  }
   float* part = (float*)ws;
   if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);

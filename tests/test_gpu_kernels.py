@@ -537,11 +537,13 @@ def test_argmax_nan_logits_stay_in_bounds():
 
 
 # ------------------------------------------------------------------ prefill GEMM
-# (512, 9216, 2560): 64x64 tiles, one LDS stage; (512, 2560, 9216): two stages,
-# two K blocks in flight; (5, 256, 384): odd K-block count;
-# (700, 9000, 2560): ragged one-stage tiles; (2000, 4100, 384): ragged 128x128
-# tiles; (128, 2560, 4096), (37, 1000, 9216), (128, 32, 2560): split-K in 8, 8
-# (ragged N, one M tile) and 5.
+# Without a workspace every shape runs the persistent ring kernel: (512, 9216,
+# 2560) and (512, 2560, 9216) are config 3a (several tiles per workgroup);
+# (5, 256, 384) an odd K-block count; (130, 200, 256), (700, 9000, 2560),
+# (2000, 4100, 384) ragged M and N (rows past M / N read as zeros).  With a
+# workspace, (128, 2560, 4096), (37, 1000, 9216) and (128, 32, 2560) split K in
+# 8, 8 and 5 (split-K kernel + reduction); the others have more tiles than
+# CUs and take the ring kernel again.
 @pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256),
                                    (700, 9000, 2560), (2000, 4100, 384), (128, 2560, 4096),
                                    (37, 1000, 9216), (128, 32, 2560)])
@@ -560,6 +562,14 @@ def test_gemm_e4m3(M, N, K):
     sync()
     ref16 = x.float() @ orc.dequant(w, s.to(torch.bfloat16).float()).t()
     assert cos_sim(y16.cpu().float(), ref16) >= 0.99999
+    lib = abi.load()
+    ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
+    yw = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemm_e4m3(abi.ptr(cu(x)), abi.ptr(cu(w)), abi.ptr(cu(s)), abi.ptr(yw), M, N, K,
+                               K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm with workspace")
+    sync()
+    assert cos_sim(yw.cpu().float(), ref) >= 0.99999
+    assert_close(yw, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="gemm, workspace")
 
 
 @pytest.mark.parametrize("M", [128, 37])
