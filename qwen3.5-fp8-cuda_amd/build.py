@@ -65,7 +65,9 @@ def build(jobs=None, debug=False, verbose=True):
         for f in futs:
             f.result()
     tmp = LIB_PATH + ".tmp"
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # -z defs: an unresolved symbol (e.g. a kernel launch stub the host pass
+    # failed to emit) fails the link instead of the first dlopen
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
