@@ -211,9 +211,10 @@ def time_prefill_gemm(reps=20):
                     "frac_bf16_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)})
     return {"config": "BASELINE configs[2]: X[512x2560] x W[9216x2560]^T and X'[512x9216] x "
                       "W'[2560x9216]^T, E4M3 128x128 block scales, seed 0",
-            "kernel": "gemm_e4m3_lds_kernel (v_mfma_f32_32x32x16_bf16: E4M3 weights widened exactly "
-                      "to bf16 as they leave LDS, bf16 activations as is, fp32 products and "
-                      "accumulation; no workspace)",
+            "kernel": "gemm_dma_kernel (persistent workgroups, 64x64 tiles through a direct-to-LDS "
+                      "ring; v_mfma_f32_32x32x16_bf16 with E4M3 weights widened exactly to bf16 as "
+                      "they leave LDS, bf16 activations as is, fp32 products and accumulation; "
+                      "no workspace)",
             "peak_tflops": BF16_MFMA_PEAK_TFLOPS, "gemms": res}
 
 
