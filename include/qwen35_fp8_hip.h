@@ -171,6 +171,14 @@ int qh_mlp_decode(const void* h, const void* o, const float* norm_w, float eps, 
 int qh_rmsnorm(const void* x, const float* w, void* out, int rows, int D, float eps,
                qh_stream_t stream);
 
+/* Residual add + (1+w) RMSNorm of `rows` rows of D: h = bf16(h + o) in place,
+ * out = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w)); out must not alias h or o.
+ * No reference counterpart: it fuses elem_add_kernel (fused_kernels.cu:553-559)
+ * and the (1+w) RMSNorm (fused_kernels.cu:489-547) that main.py's prefill runs
+ * back to back after every output projection (main.py:1550-1566). */
+int qh_add_rmsnorm(void* h, const void* o, const float* w, void* out, int rows, int D, float eps,
+                   qh_stream_t stream);
+
 /* Scratch bytes for qh_attn_decode with nsplit > 1. */
 size_t qh_attn_scratch_bytes(int n_kv_heads, int nsplit, int head_dim);
 

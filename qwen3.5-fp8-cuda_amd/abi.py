@@ -63,6 +63,7 @@ NATIVE_SIGNATURES = {
     "qh_mlp_decode": (_i, [_vp, _vp, _vp, _f, _i, _vp, _vp, _vp, _vp, _i, _i,
                            _vp, _vp, _i, _vp, _vp, _i, _vp]),
     "qh_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "qh_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _vp]),
     "qh_attn_scratch_bytes": (_sz, [_i, _i, _i]),
     "qh_attn_decode": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                             _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _f, _vp]),

@@ -482,6 +482,24 @@ QH_EXPORT int qh_rmsnorm(const void* x, const float* w, void* out, int rows, int
   return check_launch("qh_rmsnorm");
 }
 
+QH_EXPORT int qh_add_rmsnorm(void* h, const void* o, const float* w, void* out, int rows, int D,
+                             float eps, hipStream_t stream) {
+  if (rows < 0 || D <= 0) {
+    qh_set_error("qh_add_rmsnorm: bad shape rows=%d D=%d", rows, D);
+    return -1;
+  }
+  if (rows > 0 && (!h || !o || !w || !out)) {
+    qh_set_error("qh_add_rmsnorm: null pointer");
+    return -1;
+  }
+  if (out == h || out == o) {
+    qh_set_error("qh_add_rmsnorm: out must not alias h or o");
+    return -1;
+  }
+  qh_launch_add_rmsnorm_rows(h, o, w, out, rows, D, eps, stream);
+  return check_launch("qh_add_rmsnorm");
+}
+
 QH_EXPORT size_t qh_attn_scratch_bytes(int n_kv_heads, int nsplit, int head_dim) {
   return qh_attn_scratch_floats(n_kv_heads, nsplit, head_dim) * sizeof(float);
 }

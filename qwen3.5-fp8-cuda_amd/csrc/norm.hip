@@ -10,7 +10,9 @@
 //    rounding points of main.py's torch path (bf16 after the norm, after the
 //    weight product and after silu(z)); otherwise everything stays fp32 and
 //    only the output is rounded, like the reference's fused kernel.
-//  * bf16 residual add and embedding-row gather.
+//  * bf16 residual add, fused residual add + (1+w) RMSNorm of whole rows (the
+//    batch prefill's pattern after every out_proj / o_proj / down), and
+//    embedding-row gather.
 #include "qh_common.h"
 #include "qh_norm.h"
 
@@ -68,6 +70,65 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* core
   out[off] = f2bf(y);
 }
 
+// Residual add + (1+w) RMSNorm of whole rows, one 256-thread block per row:
+//   h = bf16(h + o)  (stored back when o is given), out = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w)),
+// the rounding points of the reference's separate add and norm
+// (fused_kernels.cu:553-559, 489-547).  Each thread holds up to V 8-element
+// vectors of the row in registers, so the row is read once with 16-byte loads.
+// Requires D % 8 == 0, D <= 2048 V and 16-byte aligned rows and weights.
+template <int V>
+__global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(uint16_t* h, const uint16_t* o, const float* w,
+                                                               uint16_t* out, int D, float eps) {
+  __shared__ float red[4];
+  const int t = threadIdx.x, nv = D >> 3;
+  uint16_t* hr = h + (size_t)blockIdx.x * D;
+  const uint16_t* orow = o ? o + (size_t)blockIdx.x * D : nullptr;
+  float xv[V][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int i = t + 256 * v;
+    if (i < nv) {
+      u32x4 a = *(const u32x4*)(hr + 8 * i);
+      if (orow) {
+        const u32x4 b = *(const u32x4*)(orow + 8 * i);
+        u32x4 sum;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = rbf(bf_lo(a[q]) + bf_lo(b[q])), hi = rbf(bf_hi(a[q]) + bf_hi(b[q]));
+          sum[q] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+        }
+        a = sum;
+        *(u32x4*)(hr + 8 * i) = a;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xv[v][2 * q] = bf_lo(a[q]);
+        xv[v][2 * q + 1] = bf_hi(a[q]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xv[v][e], xv[v][e], ss);
+    }
+  }
+  ss = block_sum_256(ss, red);
+  const float rms = rsqrtf(ss / (float)D + eps);
+  uint16_t* yr = out + (size_t)blockIdx.x * D;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int i = t + 256 * v;
+    if (i < nv) {
+      const float4 w0 = *(const float4*)(w + 8 * i), w1 = *(const float4*)(w + 8 * i + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      u32x4 y;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        y[q] = (uint32_t)f2bf(xv[v][2 * q] * rms * (1.0f + wv[2 * q])) |
+               ((uint32_t)f2bf(xv[v][2 * q + 1] * rms * (1.0f + wv[2 * q + 1])) << 16);
+      *(u32x4*)(yr + 8 * i) = y;
+    }
+  }
+}
+
 __global__ void add_bf16_kernel(const uint16_t* a, const uint16_t* b, uint16_t* out, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = f2bf(bf2f(a[i]) + bf2f(b[i]));
@@ -85,10 +146,45 @@ __global__ void embed_gather_kernel(const uint16_t* table, const int64_t* ids, u
 
 }  // namespace
 
+namespace {
+bool rows_vectorizable(const void* a, const void* b, const void* w, const void* out, int D) {
+  const auto al = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
+  return D % 8 == 0 && D <= 2048 * 4 && al(a) && al(b) && al(w) && al(out);
+}
+
+template <int V>
+void launch_add_rmsnorm_v(void* h, const void* o, const float* w, void* out, int rows, int D, float eps,
+                          hipStream_t st) {
+  hipLaunchKernelGGL((add_rmsnorm_rows_kernel<V>), dim3(rows), dim3(256), 0, st, (uint16_t*)h,
+                     (const uint16_t*)o, w, (uint16_t*)out, D, eps);
+}
+
+// The vector kernel for D <= 8192 (8 elements per thread per vector).
+bool launch_add_rmsnorm_vec(void* h, const void* o, const float* w, void* out, int rows, int D, float eps,
+                            hipStream_t st) {
+  if (!rows_vectorizable(h, o, w, out, D)) return false;
+  const int v = (D / 8 + 255) / 256;
+  if (v <= 1) launch_add_rmsnorm_v<1>(h, o, w, out, rows, D, eps, st);
+  else if (v == 2) launch_add_rmsnorm_v<2>(h, o, w, out, rows, D, eps, st);
+  else launch_add_rmsnorm_v<4>(h, o, w, out, rows, D, eps, st);
+  return true;
+}
+}  // namespace
+
 void qh_launch_rmsnorm_rows(const void* x, const float* w, void* out, int rows, int D, float eps,
                             hipStream_t st) {
   if (rows <= 0) return;
+  if (launch_add_rmsnorm_vec(const_cast<void*>(x), nullptr, w, out, rows, D, eps, st)) return;
   hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, (const uint16_t*)x, w,
+                     (uint16_t*)out, D, eps);
+}
+
+void qh_launch_add_rmsnorm_rows(void* h, const void* o, const float* w, void* out, int rows, int D,
+                                float eps, hipStream_t st) {
+  if (rows <= 0) return;
+  if (launch_add_rmsnorm_vec(h, o, w, out, rows, D, eps, st)) return;
+  qh_launch_add_bf16(h, o, h, rows * D, st);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, (const uint16_t*)h, w,
                      (uint16_t*)out, D, eps);
 }
 

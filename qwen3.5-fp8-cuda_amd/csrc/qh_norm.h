@@ -6,6 +6,9 @@
 
 void qh_launch_rmsnorm_rows(const void* x, const float* w, void* out, int rows, int D, float eps,
                             hipStream_t st);
+// h = bf16(h + o) in place, out = (1+w) RMSNorm of h; out must not alias h or o.
+void qh_launch_add_rmsnorm_rows(void* h, const void* o, const float* w, void* out, int rows, int D,
+                                float eps, hipStream_t st);
 void qh_launch_linear_gates(const void* a, const void* b, const float* A_log, const float* dt_bias,
                             float* g_out, void* beta_out, int heads, hipStream_t st);
 void qh_launch_gated_rmsnorm(const void* core, const void* z, const void* w, void* out, int heads,

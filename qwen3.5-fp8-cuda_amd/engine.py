@@ -455,10 +455,13 @@ class Qwen35FP8Engine:
         B["ids"][:M].copy_(ids)
         abi.check(L.qh_embed(abi.ptr(self.w.embed), abi.ptr(B["ids"]), abi.ptr(h), M, H,
                              cfg.vocab_size, st), "embed")
+        # Each residual add is fused with the (1+w) RMSNorm that follows it
+        # (qh_add_rmsnorm); layer 0's input norm stands alone and the last
+        # layer's final add has no norm after it (lm_head applies norm_f).
+        abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(self.w.layers[0]["input_layernorm"]), abi.ptr(hn),
+                               M, H, eps, st), "rmsnorm")
         for i in range(cfg.num_hidden_layers):
             ly = self.w.layers[i]
-            abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(ly["input_layernorm"]), abi.ptr(hn), M, H,
-                                   eps, st), "rmsnorm")
             if cfg.is_full(i):
                 D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
                 q_all, k, v = B["q_all"][:M], B["k"][:M], B["v"][:M]
@@ -496,15 +499,19 @@ class Qwen35FP8Engine:
                 else:
                     abi.check(L.qh_gdn_scan(*scan_args, st), "gdn_scan")
                 self._gemm(B["gated"][:M], ly["out_proj"], o, M, ws)
-            abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
-            abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(ly["post_attention_layernorm"]),
-                                   abi.ptr(hn), M, H, eps, st), "rmsnorm")
+            abi.check(L.qh_add_rmsnorm(abi.ptr(h), abi.ptr(o), abi.ptr(ly["post_attention_layernorm"]),
+                                       abi.ptr(hn), M, H, eps, st), "add_rmsnorm")
             self._gemm_group(hn, [(ly["gate_proj"], B["gu_g"][:M]), (ly["up_proj"], B["gu_u"][:M])],
                              M, ws)
             abi.check(L.qh_silu_mul(abi.ptr(B["gu_g"]), abi.ptr(B["gu_u"]), abi.ptr(B["m"]), M * I,
                                     st), "silu_mul")
             self._gemm(B["m"][:M], ly["down_proj"], o, M, ws)
-            abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
+            if i + 1 < cfg.num_hidden_layers:
+                abi.check(L.qh_add_rmsnorm(abi.ptr(h), abi.ptr(o),
+                                           abi.ptr(self.w.layers[i + 1]["input_layernorm"]), abi.ptr(hn),
+                                           M, H, eps, st), "add_rmsnorm")
+            else:
+                abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
             if trace is not None:
                 trace.append(h[M - 1].float().cpu())
         out = None

@@ -70,6 +70,13 @@ def test_validation_errors_need_no_gpu():
     assert rc == -1 and "multiple of 8" in abi.last_error()
     rc = lib.qh_rmsnorm(None, None, None, 1, 0, 1e-6, None)
     assert rc == -1 and "bad shape" in abi.last_error()
+    rc = lib.qh_add_rmsnorm(None, None, None, None, -1, 2560, 1e-6, None)
+    assert rc == -1 and "bad shape" in abi.last_error()
+    rc = lib.qh_add_rmsnorm(None, None, None, None, 4, 2560, 1e-6, None)
+    assert rc == -1 and "null pointer" in abi.last_error()
+    p = ctypes.c_void_p(4096)
+    rc = lib.qh_add_rmsnorm(p, ctypes.c_void_p(8192), ctypes.c_void_p(12288), p, 4, 2560, 1e-6, None)
+    assert rc == -1 and "alias" in abi.last_error()
     rc = lib.qh_gated_rmsnorm(None, None, None, None, 4, 512, 1e-6, 1, None)
     assert rc == -1 and "head_dim" in abi.last_error()
     rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,

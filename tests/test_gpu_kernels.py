@@ -185,6 +185,35 @@ def test_rmsnorm_reference_abi():
         assert torch.equal(xg.cpu(), out.cpu())
 
 
+@pytest.mark.parametrize("M,D", [(128, 2560), (3, 256), (5, 8192), (7, 1000), (4, 100)])
+def test_add_rmsnorm(M, D):
+    """qh_add_rmsnorm (the batch prefill's residual add + (1+w) RMSNorm after
+    every output projection): h = bf16(h + o) bit for bit, out against the
+    oracle's rmsnorm of that sum.  D = 2560 / 256 / 8192 / 1000 take the 16-byte
+    vector kernel (1, 2 or 4 vectors per thread, a partial last vector row);
+    D = 100 (not a multiple of 8) the scalar fallback."""
+    g = gen(M * 31 + D)
+    h = bf(randn(g, M, D) * 2)
+    o = bf(randn(g, M, D))
+    w = randn(g, D, std=0.02)
+    want_h = bf(h.float() + o.float())
+    ref = orc.rmsnorm(want_h.float(), w)
+    hg, og, wg = cu(h), cu(o), cu(w)
+    out = torch.empty_like(hg)
+    lib = abi.load()
+    abi.check(lib.qh_add_rmsnorm(abi.ptr(hg), abi.ptr(og), abi.ptr(wg), abi.ptr(out), M, D, 1e-6,
+                                 abi.stream_handle()), "add_rmsnorm")
+    sync()
+    assert torch.equal(hg.cpu(), want_h), "residual sum differs from the bf16 add"
+    assert_close(out, ref, what="add_rmsnorm")
+    # the plain norm on the same rows goes through the same kernel (o = null)
+    out2 = torch.empty_like(hg)
+    abi.check(lib.qh_rmsnorm(abi.ptr(hg), abi.ptr(wg), abi.ptr(out2), M, D, 1e-6, abi.stream_handle()),
+              "rmsnorm")
+    sync()
+    assert torch.equal(out2.cpu(), out.cpu())
+
+
 # ------------------------------------------------------------------ MLP
 @pytest.mark.parametrize("H,I", [(2560, 9216), (256, 512)])
 def test_mlp_decode(H, I):
