@@ -21,12 +21,13 @@
 // Two kernels, both on 64 x 64 output tiles (a 2 x 2 grid of waves, each one
 // 32x32 matrix-core tile) in an XCD-aware tile order (the row tiles of one
 // weight tile run on one XCD and share it in that XCD's L2):
-//  - gemm_dma_kernel (every unsplit launch): persistent workgroups, three per
-//    CU, stream (tile, K block) units through a two-stage LDS ring filled by
-//    direct-to-LDS loads;
-//  - gemm_e4m3_lds_kernel (split-K): one workgroup per (tile, K slice), the
-//    next K blocks in registers while the current one is multiplied, fp32
-//    partials finished by gemm_splitk_reduce_kernel.
+//  - gemm_dma_kernel (every launch whose operands it can take): persistent
+//    workgroups, three per CU, stream (tile or tile K slice, K block) units
+//    through a two-stage LDS ring filled by direct-to-LDS loads; split-K
+//    partials are finished by gemm_splitk_reduce_kernel;
+//  - gemm_e4m3_lds_kernel (fallback for unaligned weights or scales): one
+//    workgroup per (tile, K slice), the next K blocks in registers while the
+//    current one is multiplied.
 // Operand layout of the 32x32x16 bf16 instruction (measured on gfx950):
 // lane l holds A[l % 32][8 (l / 32) + r] and B[8 (l / 32) + r][l % 32],
 // r = 0..7, and accumulator value e is C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
@@ -281,9 +282,10 @@ __device__ __forceinline__ void lds_wait(u32x4& a, u32x2& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
 }
 
-// One tile of the walk and its segment, all workgroup-uniform.
+// One work item of the walk (a tile, or with split-K one K slice of a tile)
+// and its segment, all workgroup-uniform.
 struct DmaTile {
-  int tn, tm, nb, N, kb_code, sbytes;
+  int tn, tm, nb, N, kb_code, sbytes, kb0;
   const uint8_t* w;
   const void* s;
   uint16_t* y;
@@ -291,8 +293,12 @@ struct DmaTile {
 
 // The group is indexed in place (a kernel argument: scalar loads), never
 // copied to a local array.
-__device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m) {
+// Item i of XCD xc: K slice i % S (K blocks kb0 .. kb0 + KBs - 1) of tile
+// i / S, whose row tile is fastest.
+__device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m, int S, int KBs) {
   DmaTile d;
+  d.kb0 = (i % S) * KBs;
+  i /= S;
   d.tn = xc + 8 * (i / tiles_m);
   d.tm = i % tiles_m;
   int si = 0;
@@ -309,20 +315,24 @@ __device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, i
   return d;
 }
 
-template <typename ScaleT, int DS>
+// S > 1: each item is one K slice of a tile and its fp32 partial tile goes to
+// part[(slice M + m) ldp + global column] for gemm_splitk_reduce_kernel.
+template <typename ScaleT, int DS, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGroup g, int M, int K,
-                                                       int tiles_n, int tiles_m) {
+                                                       int tiles_n, int tiles_m, int S_arg, float* part,
+                                                       int ldp) {
+  const int S = SPLIT ? S_arg : 1;  // unsplit launches compile without the slice arithmetic
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int wm = (wid >> 1) * 32, wn = (wid & 1) * 32;
-  const int KB = K / 128;
-  // this workgroup's tiles: XCD xc, its j-th of P workgroups there; XCD xc
-  // owns N tiles xc, xc + 8, ... with all their row tiles (row tile fastest),
-  // dealt round-robin to its workgroups
+  const int KB = K / 128 / S;  // K blocks per item
+  // this workgroup's items: XCD xc, its j-th of P workgroups there; XCD xc
+  // owns N tiles xc, xc + 8, ... with all their row tiles (row tile fastest)
+  // and K slices, dealt round-robin to its workgroups
   const int xc = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3, P = (int)gridDim.x >> 3;
-  const int ntx = tiles_n > xc ? tiles_m * ((tiles_n - xc + 7) / 8) : 0;
+  const int ntx = tiles_n > xc ? tiles_m * ((tiles_n - xc + 7) / 8) * S : 0;
   const int my_tiles = j < ntx ? (ntx - j + P - 1) / P : 0;
   const int U = my_tiles * KB;
   if (U == 0) return;
@@ -344,7 +354,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   // issue cursor: the unit whose loads go out next (it stays on the last unit
   // once reached, so the ring keeps DS - 1 units of loads outstanding)
   int it = 0, ikb = 0;
-  DmaTile itile = dma_tile(g, xc, j, tiles_m);
+  DmaTile itile = dma_tile(g, xc, j, tiles_m, S, KB);
   rsrc_t rx, rw, rs;
   auto bind = [&]() {
     const int rows_m = min(M - itile.tm * 64, 64), rows_n = min(itile.N - itile.nb, 64);
@@ -357,7 +367,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   bind();
   auto issue = [&](int st) {
     uint8_t* stage = smem + st * kDStage;
-    const uint32_t ko = (uint32_t)ikb * 256u;
+    const int kb = itile.kb0 + ikb;
+    const uint32_t ko = (uint32_t)kb * 256u;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + (16 * wid + 4 * i) * 256), 16, xo[i] + ko,
@@ -368,7 +379,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
                                                wo[i] + (ko >> 1), 0, 0, 0);
     // scales of this wave's 32 columns (lanes 32-63 repeat them), as the
     // aligned words holding them
-    const int si = scale_index(itile.kb_code, min(itile.nb + wn + r, itile.N - 1), ikb);
+    const int si = scale_index(itile.kb_code, min(itile.nb + wn + r, itile.N - 1), kb);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + kDA + kDB + wid * 256), 4,
                                              ((uint32_t)si * (uint32_t)sizeof(ScaleT)) & ~3u, 0, 0, 0);
   };
@@ -378,7 +389,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     } else if (it + 1 < my_tiles) {
       ++it;
       ikb = 0;
-      itile = dma_tile(g, xc, j + it * P, tiles_m);
+      itile = dma_tile(g, xc, j + it * P, tiles_m, S, KB);
       bind();
     }
   };
@@ -391,7 +402,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
 
   // compute cursor
   int ckb = 0, ct = 0;
-  DmaTile ctile = dma_tile(g, xc, j, tiles_m);
+  DmaTile ctile = dma_tile(g, xc, j, tiles_m, S, KB);
   v16f acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
@@ -428,21 +439,31 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     if constexpr (sizeof(ScaleT) == 4) {
       scale = __uint_as_float(sw);
     } else {
-      const int idx = scale_index(ctile.kb_code, min(ctile.nb + wn + r, ctile.N - 1), ckb);
+      const int idx = scale_index(ctile.kb_code, min(ctile.nb + wn + r, ctile.N - 1), ctile.kb0 + ckb);
       scale = (idx & 1) ? bf_hi(sw) : bf_lo(sw);
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = fmaf(t[e], scale, acc[e]);
-    if (++ckb == KB) {  // the tile is complete: store it, start the next one
+    if (++ckb == KB) {  // the item is complete: store it, start the next one
       const int n = ctile.nb + wn + r;
+      if constexpr (SPLIT) {
+        float* pz = part + (size_t)(ctile.kb0 / KB) * M * ldp + ctile.tn * 64 + wn + r;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[e]);
-        acc[e] = 0.0f;
+        for (int e = 0; e < 16; ++e) {
+          const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < M) pz[(size_t)m * ldp] = acc[e];
+          acc[e] = 0.0f;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[e]);
+          acc[e] = 0.0f;
+        }
       }
       ckb = 0;
-      if (++ct < my_tiles) ctile = dma_tile(g, xc, j + ct * P, tiles_m);
+      if (++ct < my_tiles) ctile = dma_tile(g, xc, j + ct * P, tiles_m, S, KB);
     }
     st = st == DS - 1 ? 0 : st + 1;
   }
@@ -454,9 +475,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
 // of K bf16) stay below 2^31 bytes.
 inline bool gemm_dma_fits(int K) { return (long)64 * K * 2 < 0x7fffffffL; }
 
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
+                                                                 int ldp, GemmGroup g, int bn);
+
 template <typename ScaleT, int DS>
 void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, hipStream_t st,
-                     int cus, int wpc) {
+                     int cus, int wpc, int S = 1, float* part = nullptr) {
   GemmGroup g = {};
   g.nseg = nseg;
   int tiles_n = 0;
@@ -477,11 +501,21 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
   // P workgroups per XCD: as many as the busiest XCD has tiles (XCD 0 owns
   // ceil(tiles_n / 8) N tiles), at most wpc per CU, so no workgroup there
   // takes a second tile while others are idle
-  const long busiest = (long)tiles_m * ((tiles_n + 7) / 8);
+  const long busiest = (long)tiles_m * ((tiles_n + 7) / 8) * S;
   const int P = (int)max(1L, min((long)cus * wpc / 8, busiest));
   const int G = 8 * P;
-  hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g, M, K,
-                     tiles_n, tiles_m);
+  const int ldp = tiles_n * 64;
+  if (S > 1)
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g,
+                       M, K, tiles_n, tiles_m, S, part, ldp);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g,
+                       M, K, tiles_n, tiles_m, 1, nullptr, ldp);
+  if (S > 1) {
+    const size_t quads = (size_t)M * ldp / 4;
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st,
+                       (const float*)part, S, M, ldp, g, 64);
+  }
 }
 
 // Split-K finish: y = bf16(sum_z part[z][m][column]), summed in z order;
@@ -614,18 +648,19 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
       S = c;
       break;
     }
-  // Unsplit: the persistent ring kernel, three workgroups per CU (two 25 KB
-  // stages each), when its direct-to-LDS loads can take the operands as they
-  // are (16-byte aligned weights, word-aligned scales, tile ranges < 2 GiB).
-  bool ring = S == 1 && gemm_dma_fits(K);
+  float* part = (float*)ws;
+  // The persistent ring kernel, three workgroups per CU (two 25 KB stages
+  // each), split or not, when its direct-to-LDS loads can take the operands as
+  // they are (16-byte aligned weights, word-aligned scales, tile ranges
+  // < 2 GiB); the per-workgroup kernel otherwise.
+  bool ring = gemm_dma_fits(K);
   for (int t = 0; t < nseg; ++t)
     ring = ring && (uintptr_t)seg[t].w % 16 == 0 && (uintptr_t)seg[t].s % 4 == 0;
   if (ring) {
-    if (scale_bf16) launch_gemm_dma<uint16_t, 2>(xa, seg, nseg, M, K, st, cus, 3);
-    else launch_gemm_dma<float, 2>(xa, seg, nseg, M, K, st, cus, 3);
+    if (scale_bf16) launch_gemm_dma<uint16_t, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
+    else launch_gemm_dma<float, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
     return 0;
   }
-  float* part = (float*)ws;
   if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   return 0;
