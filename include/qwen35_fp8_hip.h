@@ -298,6 +298,17 @@ size_t qh_gemm_workspace_size(int M, int K);
 int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
                  int kb, int scales_bf16, void* ws, qh_stream_t stream);
 
+/* Output projection + residual add + (1+w) RMSNorm, the batch prefill's step
+ * after o_proj / out_proj / down: o = bf16(x . deq(W)^T) (M x N scratch, not
+ * written when the split-K finish fuses all three), h = bf16(h + o) in place,
+ * hn = bf16(h * rsqrt(mean(h^2) + eps) * (1 + norm_w)); norm_w null: the add
+ * only.  x, o, h, hn distinct; ws as qh_gemm_e4m3 (null: no split).  No
+ * reference counterpart: main.py:1550-1566 runs fp8_gemm_batch, the add and
+ * the norm as separate steps. */
+int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
+                             int kb, int scales_bf16, void* h, const float* norm_w, void* hn, float eps,
+                             void* ws, qh_stream_t stream);
+
 /* Grouped prefill GEMM; no counterpart in the reference, which runs each
  * projection as its own fp8_gemm_batch (main.py:262-269).  Up to 4 projections
  * of one activation x [M, K] (segment t: y_t [M, n_t] = bf16(x . deq(w_t)^T),

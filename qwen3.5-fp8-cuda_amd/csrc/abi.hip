@@ -752,6 +752,37 @@ QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y,
   return check_launch("qh_gemm_e4m3");
 }
 
+// Output projection + residual add + (1+w) RMSNorm (no reference counterpart:
+// main.py's prefill runs fp8_gemm_batch, the add and the norm as three steps,
+// main.py:1550-1566).  o = bf16(x W^T) (scratch; not written when the split-K
+// finish does all three), h = bf16(h + o) in place, hn = RMSNorm(h) with
+// (1 + norm_w) (norm_w null: the add only).
+QH_EXPORT int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
+                                       int kb, int scales_bf16, void* h, const float* norm_w, void* hn, float eps,
+                                       void* ws, hipStream_t stream) {
+  if (K <= 0 || K % 128 != 0) {
+    qh_set_error("qh_gemm_e4m3_add_rmsnorm: K=%d must be a positive multiple of 128", K);
+    return -1;
+  }
+  if (M < 0 || N < 0) {
+    qh_set_error("qh_gemm_e4m3_add_rmsnorm: bad shape M=%d N=%d", M, N);
+    return -1;
+  }
+  if (M == 0 || N == 0) return 0;
+  if (!x || !w || !s || !o || !h || (norm_w && !hn)) {
+    qh_set_error("qh_gemm_e4m3_add_rmsnorm: null pointer");
+    return -1;
+  }
+  if (o == h || o == x || h == x || (norm_w && (hn == h || hn == o || hn == x))) {
+    qh_set_error("qh_gemm_e4m3_add_rmsnorm: x, o, h and hn must be distinct buffers");
+    return -1;
+  }
+  if (qh_launch_gemm_e4m3_add_rmsnorm(x, w, s, o, M, N, K, kb, scales_bf16 != 0, h, norm_w, hn, eps, ws,
+                                      stream) != 0)
+    return -1;
+  return check_launch("qh_gemm_e4m3_add_rmsnorm");
+}
+
 // Grouped prefill GEMM (no reference counterpart: the reference runs each
 // projection as its own fp8_gemm_batch, main.py:262-269).  Up to 4
 // projections of the same activation X[M, K] -- segment t:

@@ -33,6 +33,7 @@
 // r = 0..7, and accumulator value e is C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
 #include "qh_common.h"
 #include "qh_gemm.h"
+#include "qh_norm.h"
 
 namespace {
 
@@ -478,9 +479,10 @@ inline bool gemm_dma_fits(int K) { return (long)64 * K * 2 < 0x7fffffffL; }
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
                                                                  int ldp, GemmGroup g, int bn);
 
+// reduce = false leaves split-K partials for the caller's own finishing kernel.
 template <typename ScaleT, int DS>
 void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, hipStream_t st,
-                     int cus, int wpc, int S = 1, float* part = nullptr) {
+                     int cus, int wpc, int S = 1, float* part = nullptr, bool reduce = true) {
   GemmGroup g = {};
   g.nseg = nseg;
   int tiles_n = 0;
@@ -511,7 +513,7 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
   else
     hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g,
                        M, K, tiles_n, tiles_m, 1, nullptr, ldp);
-  if (S > 1) {
+  if (S > 1 && reduce) {
     const size_t quads = (size_t)M * ldp / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st,
                        (const float*)part, S, M, ldp, g, 64);
@@ -539,6 +541,67 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* pa
 #pragma unroll
   for (int c = 0; c < 4; ++c)
     if (n + c < N) y[c] = f2bf(acc[c]);
+}
+
+// Split-K finish fused with the residual add and the (1+w) RMSNorm that follow
+// an output projection, one 256-thread block per row m of one N-wide segment:
+//   o = bf16(sum_z part[z][m][:N])  (z in order, as gemm_splitk_reduce_kernel),
+//   h = bf16(h + o) in place, hn = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w))
+// (no hn when w is null).  V 8-column vectors per thread stay in registers;
+// requires N % 8 == 0, N <= 2048 V and 16-byte aligned rows.
+template <int V>
+__global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* part, int S, int M, int ldp, int N,
+                                                                 uint16_t* h, const float* w, uint16_t* hn,
+                                                                 float eps) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x, nv = N >> 3;
+  uint16_t* hr = h + (size_t)m * N;
+  float xv[V][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int i = t + 256 * v;
+    if (i < nv) {
+      const float* p0 = part + (size_t)m * ldp + 8 * i;
+      f32x4 a0 = *(const f32x4*)p0, a1 = *(const f32x4*)(p0 + 4);
+      for (int z = 1; z < S; ++z) {
+        const float* pz = p0 + (size_t)z * M * ldp;
+        a0 += *(const f32x4*)pz;
+        a1 += *(const f32x4*)(pz + 4);
+      }
+      const u32x4 hv = *(const u32x4*)(hr + 8 * i);
+      u32x4 sum;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float o_lo = rbf(q < 2 ? a0[2 * q] : a1[2 * q - 4]);
+        const float o_hi = rbf(q < 2 ? a0[2 * q + 1] : a1[2 * q - 3]);
+        xv[v][2 * q] = rbf(bf_lo(hv[q]) + o_lo);
+        xv[v][2 * q + 1] = rbf(bf_hi(hv[q]) + o_hi);
+        sum[q] = (__float_as_uint(xv[v][2 * q]) >> 16) | (__float_as_uint(xv[v][2 * q + 1]) & 0xFFFF0000u);
+      }
+      *(u32x4*)(hr + 8 * i) = sum;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xv[v][e], xv[v][e], ss);
+    }
+  }
+  if (!w) return;
+  ss = block_sum_256(ss, red);
+  const float rms = rsqrtf(ss / (float)N + eps);
+  uint16_t* yr = hn + (size_t)m * N;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int i = t + 256 * v;
+    if (i < nv) {
+      const float4 w0 = *(const float4*)(w + 8 * i), w1 = *(const float4*)(w + 8 * i + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      u32x4 y;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        y[q] = (uint32_t)f2bf(xv[v][2 * q] * rms * (1.0f + wv[2 * q])) |
+               ((uint32_t)f2bf(xv[v][2 * q + 1] * rms * (1.0f + wv[2 * q + 1])) << 16);
+      *(u32x4*)(yr + 8 * i) = y;
+    }
+  }
 }
 
 template <int BN>
@@ -599,6 +662,20 @@ void launch_gemm_small(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M,
 // 64x64 fp32 partials, so this covers up to 1024 of them (341 CUs).
 constexpr size_t kSplitPartBytes = (size_t)1024 * 64 * 64 * sizeof(float);
 
+namespace {
+// Split-K (caller workspace only) when there are no more tiles than CUs: the
+// largest S <= 8 dividing the K blocks with >= 4 blocks per slice and
+// S * tiles <= 3 per CU, so each workgroup walks fewer serial K steps.
+int gemm_split_count(int K, long tiles, int cus, const void* ws) {
+  const int KB = K / 128;
+  for (int c = 8; ws && c >= 2 && tiles <= cus; --c)
+    if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
+        (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes)
+      return c;
+  return 1;
+}
+}  // namespace
+
 size_t qh_gemm_workspace_bytes(int M, int K) {
   (void)M;
   (void)K;
@@ -637,17 +714,7 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   // occupancy or (weights loaded straight into operand registers) the load
   // path's coalescing.
   const long tiles = tiles64 * mt;
-  // Split-K (caller workspace only) when there are no more tiles than CUs:
-  // the largest S <= 8 dividing the K blocks with >= 4 blocks per slice and
-  // S * tiles <= 3 per CU, so each workgroup walks fewer serial K steps.
-  const int KB = K / 128;
-  int S = 1;
-  for (int c = 8; ws && c >= 2 && tiles <= cus; --c)
-    if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
-        (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes) {
-      S = c;
-      break;
-    }
+  const int S = gemm_split_count(K, tiles, cus, ws);
   float* part = (float*)ws;
   // The persistent ring kernel, three workgroups per CU (two 25 KB stages
   // each), split or not, when its direct-to-LDS loads can take the operands as
@@ -663,6 +730,48 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   }
   if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
+  return 0;
+}
+
+// Output projection + residual + norm (the batch prefill's o_proj / out_proj /
+// down): o = bf16(x W^T), h = bf16(h + o), hn = (1+w) RMSNorm(h) (none when
+// norm_w is null).  When the GEMM splits K through the ring kernel and the
+// rows fit its vector kernel, one row-wise kernel finishes the split, the add
+// and the norm (o is not written); otherwise o is written and the fused
+// add + norm kernel follows.
+int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
+                                    int kb, bool scale_bf16, void* h, const float* norm_w, void* hn, float eps,
+                                    void* ws, hipStream_t st) {
+  const auto al16 = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
+  if (M > 0 && N > 0 && K > 0 && K % 128 == 0 && ws && x && (uintptr_t)x % 16 == 0 && w && s &&
+      (uintptr_t)w % 16 == 0 && (uintptr_t)s % 4 == 0 && gemm_dma_fits(K) && N % 8 == 0 && N <= 8192 &&
+      al16(h) && al16(hn) && al16(norm_w)) {
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    const long tiles = (long)((N + 63) / 64) * ((M + kBM - 1) / kBM);
+    const int S = gemm_split_count(K, tiles, cus, ws);
+    if (S > 1) {
+      const QhGemmSeg seg = {w, s, o, N, kb};
+      float* part = (float*)ws;
+      if (scale_bf16) launch_gemm_dma<uint16_t, 2>((const uint16_t*)x, &seg, 1, M, K, st, cus, 3, S, part, false);
+      else launch_gemm_dma<float, 2>((const uint16_t*)x, &seg, 1, M, K, st, cus, 3, S, part, false);
+      const int ldp = ((N + 63) / 64) * 64;
+      const int v = (N / 8 + 255) / 256;
+#define QH_SAN(V)                                                                                          \
+  hipLaunchKernelGGL((splitk_add_rmsnorm_kernel<V>), dim3(M), dim3(256), 0, st, (const float*)part, S, M, ldp, N, \
+                     (uint16_t*)h, norm_w, (uint16_t*)hn, eps)
+      if (v <= 1) QH_SAN(1);
+      else if (v == 2) QH_SAN(2);
+      else QH_SAN(4);
+#undef QH_SAN
+      return 0;
+    }
+  }
+  if (qh_launch_gemm_e4m3_ws(x, w, s, o, M, N, K, kb, scale_bf16, ws, st) != 0) return -1;
+  if (norm_w) qh_launch_add_rmsnorm_rows(h, o, norm_w, hn, M, N, eps, st);
+  else qh_launch_add_bf16(h, o, h, M * N, st);
   return 0;
 }
 

@@ -407,12 +407,16 @@ class Qwen35FP8Engine:
         }
         return self._pf
 
-    def _gemm(self, x, ws_pair, y, M, ws):
+    def _gemm_add_norm(self, x, ws_pair, o, M, ws, h, norm_w, hn):
+        """Output projection, residual add and the (1+w) RMSNorm that follows
+        (norm_w None: the add only) in qh_gemm_e4m3_add_rmsnorm: h += x W^T
+        in bf16, hn = RMSNorm(h); o is scratch."""
         w, s = ws_pair
-        abi.check(self.lib.qh_gemm_e4m3(abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M,
-                                        w.shape[0], w.shape[1], ops.scale_mode(w, s),
-                                        int(s.dtype == torch.bfloat16), abi.ptr(ws),
-                                        abi.stream_handle()), "gemm")
+        abi.check(self.lib.qh_gemm_e4m3_add_rmsnorm(
+            abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(o), M, w.shape[0], w.shape[1],
+            ops.scale_mode(w, s), int(s.dtype == torch.bfloat16), abi.ptr(h),
+            abi.ptr(norm_w) if norm_w is not None else None, abi.ptr(hn), self.eps, abi.ptr(ws),
+            abi.stream_handle()), "gemm_add_rmsnorm")
 
     def _gemm_group(self, x, segs, M, ws):
         """Projections [((w, s), y), ...] of the same activation x in one
@@ -455,9 +459,10 @@ class Qwen35FP8Engine:
         B["ids"][:M].copy_(ids)
         abi.check(L.qh_embed(abi.ptr(self.w.embed), abi.ptr(B["ids"]), abi.ptr(h), M, H,
                              cfg.vocab_size, st), "embed")
-        # Each residual add is fused with the (1+w) RMSNorm that follows it
-        # (qh_add_rmsnorm); layer 0's input norm stands alone and the last
-        # layer's final add has no norm after it (lm_head applies norm_f).
+        # Each output projection is fused with the residual add and the (1+w)
+        # RMSNorm that follow it (qh_gemm_e4m3_add_rmsnorm); layer 0's input
+        # norm stands alone and the last layer's final add has no norm after
+        # it (lm_head applies norm_f).
         abi.check(L.qh_rmsnorm(abi.ptr(h), abi.ptr(self.w.layers[0]["input_layernorm"]), abi.ptr(hn),
                                M, H, eps, st), "rmsnorm")
         for i in range(cfg.num_hidden_layers):
@@ -477,7 +482,7 @@ class Qwen35FP8Engine:
                                             2 * D, abi.ptr(self.k_cache[i]),
                                             abi.ptr(self.v_cache[i]), abi.ptr(B["att"]), M, Hq, Hkv,
                                             D, past, self.max_seq_len, st), "attn_prefill")
-                self._gemm(B["att"][:M], ly["o_proj"], o, M, ws)
+                self._gemm_add_norm(B["att"][:M], ly["o_proj"], o, M, ws, h, ly["post_attention_layernorm"], hn)
             else:
                 Hk, Hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
                 dk, dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
@@ -498,20 +503,14 @@ class Qwen35FP8Engine:
                     abi.check(L.qh_gdn_chunk(*scan_args, abi.ptr(gws), gws.numel(), st), "gdn_chunk")
                 else:
                     abi.check(L.qh_gdn_scan(*scan_args, st), "gdn_scan")
-                self._gemm(B["gated"][:M], ly["out_proj"], o, M, ws)
-            abi.check(L.qh_add_rmsnorm(abi.ptr(h), abi.ptr(o), abi.ptr(ly["post_attention_layernorm"]),
-                                       abi.ptr(hn), M, H, eps, st), "add_rmsnorm")
+                self._gemm_add_norm(B["gated"][:M], ly["out_proj"], o, M, ws, h,
+                                    ly["post_attention_layernorm"], hn)
             self._gemm_group(hn, [(ly["gate_proj"], B["gu_g"][:M]), (ly["up_proj"], B["gu_u"][:M])],
                              M, ws)
             abi.check(L.qh_silu_mul(abi.ptr(B["gu_g"]), abi.ptr(B["gu_u"]), abi.ptr(B["m"]), M * I,
                                     st), "silu_mul")
-            self._gemm(B["m"][:M], ly["down_proj"], o, M, ws)
-            if i + 1 < cfg.num_hidden_layers:
-                abi.check(L.qh_add_rmsnorm(abi.ptr(h), abi.ptr(o),
-                                           abi.ptr(self.w.layers[i + 1]["input_layernorm"]), abi.ptr(hn),
-                                           M, H, eps, st), "add_rmsnorm")
-            else:
-                abi.check(L.qh_add_bf16(abi.ptr(h), abi.ptr(o), abi.ptr(h), M * H, st), "add")
+            nxt = self.w.layers[i + 1]["input_layernorm"] if i + 1 < cfg.num_hidden_layers else None
+            self._gemm_add_norm(B["m"][:M], ly["down_proj"], o, M, ws, h, nxt, hn)
             if trace is not None:
                 trace.append(h[M - 1].float().cpu())
         out = None

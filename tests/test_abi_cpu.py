@@ -77,6 +77,16 @@ def test_validation_errors_need_no_gpu():
     p = ctypes.c_void_p(4096)
     rc = lib.qh_add_rmsnorm(p, ctypes.c_void_p(8192), ctypes.c_void_p(12288), p, 4, 2560, 1e-6, None)
     assert rc == -1 and "alias" in abi.last_error()
+    rc = lib.qh_gemm_e4m3_add_rmsnorm(None, None, None, None, 4, 2560, 100, 1, 0, None, None, None, 1e-6,
+                                      None, None)
+    assert rc == -1 and "multiple of 128" in abi.last_error()
+    rc = lib.qh_gemm_e4m3_add_rmsnorm(None, None, None, None, 4, 2560, 256, 2, 0, None, None, None, 1e-6,
+                                      None, None)
+    assert rc == -1 and "null pointer" in abi.last_error()
+    q = [ctypes.c_void_p(4096 * k) for k in range(1, 6)]
+    rc = lib.qh_gemm_e4m3_add_rmsnorm(q[0], q[1], q[2], q[3], 4, 2560, 256, 2, 0, q[3], q[4], q[0], 1e-6,
+                                      None, None)
+    assert rc == -1 and "distinct" in abi.last_error()
     rc = lib.qh_gated_rmsnorm(None, None, None, None, 4, 512, 1e-6, 1, None)
     assert rc == -1 and "head_dim" in abi.last_error()
     rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,

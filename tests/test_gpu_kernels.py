@@ -601,6 +601,51 @@ def test_gemm_e4m3(M, N, K):
     assert_close(yw, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="gemm, workspace")
 
 
+@pytest.mark.parametrize("M,N,K,norm", [(128, 2560, 4096, True), (128, 2560, 9216, True),
+                                         (37, 1000, 9216, False), (512, 2560, 9216, True),
+                                         (5, 256, 384, True), (64, 100, 256, True)])
+def test_gemm_add_rmsnorm_matches_separate_steps(M, N, K, norm):
+    """qh_gemm_e4m3_add_rmsnorm (the batch prefill's output projection +
+    residual + norm) against qh_gemm_e4m3 then qh_add_rmsnorm / qh_add_bf16
+    with the same workspace, bit for bit.  (128, 2560, 4096 / 9216) and
+    (37, 1000, 9216) split K and take the fused split-K finish; (512, 2560,
+    9216) is unsplit and (5, 256, 384) too short to split; (64, 100, 256) has
+    N % 8 != 0.  The sum is also checked against the fp32 oracle product."""
+    g = gen(M + N + K + norm)
+    w, s = quant(g, N, K)
+    x = bf(randn(g, M, K))
+    h0 = bf(randn(g, M, N))
+    nw = randn(g, N, std=0.02)
+    lib = abi.load()
+    ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
+    dx, dw, ds, dnw = cu(x), cu(w), cu(s), cu(nw)
+    # separate steps
+    o1 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    h1 = cu(h0)
+    hn1 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemm_e4m3(abi.ptr(dx), abi.ptr(dw), abi.ptr(ds), abi.ptr(o1), M, N, K, K // 128, 0,
+                               abi.ptr(ws), abi.stream_handle()), "gemm")
+    if norm:
+        abi.check(lib.qh_add_rmsnorm(abi.ptr(h1), abi.ptr(o1), abi.ptr(dnw), abi.ptr(hn1), M, N, 1e-6,
+                                     abi.stream_handle()), "add_rmsnorm")
+    else:
+        abi.check(lib.qh_add_bf16(abi.ptr(h1), abi.ptr(o1), abi.ptr(h1), M * N, abi.stream_handle()), "add")
+    # fused
+    o2 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    h2 = cu(h0)
+    hn2 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemm_e4m3_add_rmsnorm(abi.ptr(dx), abi.ptr(dw), abi.ptr(ds), abi.ptr(o2), M, N, K,
+                                           K // 128, 0, abi.ptr(h2), abi.ptr(dnw) if norm else None,
+                                           abi.ptr(hn2), 1e-6, abi.ptr(ws), abi.stream_handle()),
+              "gemm_add_rmsnorm")
+    sync()
+    assert torch.equal(h1.cpu(), h2.cpu()), "residual stream differs from the separate steps"
+    if norm:
+        assert torch.equal(hn1.cpu(), hn2.cpu()), "normed rows differ from the separate steps"
+    ref = h0.float() + orc.bf16(x.float() @ orc.dequant(w, s).t()).float()
+    assert cos_sim(h2.cpu().float(), ref) >= 0.99999
+
+
 @pytest.mark.parametrize("M", [128, 37])
 def test_gemm_grouped_matches_single_launches(M):
     """qh_gemm_e4m3_grouped (the prefill's in_proj shape: 8192 / 4096 / 32 / 32
