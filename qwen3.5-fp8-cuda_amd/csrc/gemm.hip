@@ -252,11 +252,17 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint16_t* x, G
 // wait for every outstanding ring load before each LDS read): each wave waits
 // for its own loads of the unit (vmcnt), all waves meet at a barrier, and each
 // matrix-core step waits only for its own two operand reads.
-constexpr int kDA = 64 * 256;                 // X rows of a unit: 64 x 128 bf16
-constexpr int kDB = 64 * 128;                 // W rows: 64 x 128 E4M3
-constexpr int kDSc = 4 * 256;                 // scales: one 64-word copy per wave
-constexpr int kDStage = kDA + kDB + kDSc;     // 25,600 B
-constexpr int kDLoads = 7;                    // loads per wave and unit: 4 X + 2 W + 1 scale
+// LDS of one ring stage for 64 x BN tiles: X (64 rows), W (BN rows), and one
+// 64-word copy of the column scales per wave.
+template <int BN>
+struct Ring {
+  static_assert(BN == 64 || BN == 128, "tile width");
+  static constexpr int A = 64 * 256;             // 64 X rows x 128 bf16
+  static constexpr int B = BN * 128;             // BN W rows x 128 E4M3
+  static constexpr int STAGE = A + B + 4 * 256;  // 25,600 B (BN 64), 33,792 B (BN 128)
+  static constexpr int WL = BN / 32;             // W loads (1 KB) per wave and unit
+  static constexpr int LOADS = 4 + WL + 1;       // per wave and unit: X, W, scales
+};
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -282,6 +288,10 @@ template <int N>
 __device__ __forceinline__ void lds_wait(u32x4& a, u32x2& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
 }
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, u32x4& c) {
+  asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "n"(N) : "memory");
+}
 
 // One work item of the walk (a tile, or with split-K one K slice of a tile)
 // and its segment, all workgroup-uniform.
@@ -296,6 +306,7 @@ struct DmaTile {
 // copied to a local array.
 // Item i of XCD xc: K slice i % S (K blocks kb0 .. kb0 + KBs - 1) of tile
 // i / S, whose row tile is fastest.
+template <int BN>
 __device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m, int S, int KBs) {
   DmaTile d;
   d.kb0 = (i % S) * KBs;
@@ -312,22 +323,27 @@ __device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, i
   d.N = g.N[si];
   d.kb_code = g.kb[si];
   d.sbytes = g.sbytes[si];
-  d.nb = (d.tn - g.tstart[si]) * 64;
+  d.nb = (d.tn - g.tstart[si]) * BN;
   return d;
 }
 
 // S > 1: each item is one K slice of a tile and its fp32 partial tile goes to
-// part[(slice M + m) ldp + global column] for gemm_splitk_reduce_kernel.
-template <typename ScaleT, int DS, bool SPLIT>
+// part[(slice M + m) ldp + global column] for gemm_splitk_reduce_kernel
+// (64-wide tiles only).  BN = 128: each wave holds two 32-column matrix-core
+// tiles that share its activation reads.
+template <typename ScaleT, int DS, bool SPLIT, int BN>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGroup g, int M, int K,
                                                        int tiles_n, int tiles_m, int S_arg, float* part,
                                                        int ldp) {
+  static_assert(!SPLIT || BN == 64, "split-K uses 64-wide tiles");
+  using R = Ring<BN>;
+  constexpr int NJ = BN / 64;       // 32-column matrix-core tiles per wave
   const int S = SPLIT ? S_arg : 1;  // unsplit launches compile without the slice arithmetic
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
-  const int wm = (wid >> 1) * 32, wn = (wid & 1) * 32;
+  const int wm = (wid >> 1) * 32, wn = (wid & 1) * (BN / 2);
   const int KB = K / 128 / S;  // K blocks per item
   // this workgroup's items: XCD xc, its j-th of P workgroups there; XCD xc
   // owns N tiles xc, xc + 8, ... with all their row tiles (row tile fastest)
@@ -339,26 +355,29 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   if (U == 0) return;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)smem;
 
-  // lane-constant parts of the load offsets (the unit's K block is added)
-  uint32_t xo[4], wo[2];
+  // lane-constant parts of the load offsets (the unit's K block is added);
+  // fixed-size arrays: a lambda capturing an array whose bound depends on a
+  // template parameter makes the host pass drop the kernel's launch stub
+  uint32_t xo[4], wo[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {  // X: rows 16 wid + 4 i + lane / 16
     const int row = 16 * wid + 4 * i + (lane >> 4);
     xo[i] = ((uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 15) ^ (row & 15)) * 8)) * 2u;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {  // W: rows 16 wid + 8 i + lane / 8
-    const int row = 16 * wid + 8 * i + (lane >> 3);
+  for (int i = 0; i < R::WL; ++i) {  // W: rows (BN / 4) wid + 8 i + lane / 8
+    const int row = (BN / 4) * wid + 8 * i + (lane >> 3);
     wo[i] = (uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) * 16);
   }
+  const int scol = lane & (BN / 2 - 1);  // this lane's scale column within the wave's
 
   // issue cursor: the unit whose loads go out next (it stays on the last unit
   // once reached, so the ring keeps DS - 1 units of loads outstanding)
   int it = 0, ikb = 0;
-  DmaTile itile = dma_tile(g, xc, j, tiles_m, S, KB);
+  DmaTile itile = dma_tile<BN>(g, xc, j, tiles_m, S, KB);
   rsrc_t rx, rw, rs;
   auto bind = [&]() {
-    const int rows_m = min(M - itile.tm * 64, 64), rows_n = min(itile.N - itile.nb, 64);
+    const int rows_m = min(M - itile.tm * 64, 64), rows_n = min(itile.N - itile.nb, BN);
     rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x + (size_t)itile.tm * 64 * K), (short)0,
                                            rows_m * K * 2, 0x00020000);
     rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(itile.w + (size_t)itile.nb * K), (short)0,
@@ -367,7 +386,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   };
   bind();
   auto issue = [&](int st) {
-    uint8_t* stage = smem + st * kDStage;
+    uint8_t* stage = smem + st * R::STAGE;
     const int kb = itile.kb0 + ikb;
     const uint32_t ko = (uint32_t)kb * 256u;
 #pragma unroll
@@ -375,13 +394,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + (16 * wid + 4 * i) * 256), 16, xo[i] + ko,
                                                0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + kDA + (16 * wid + 8 * i) * 128), 16,
-                                               wo[i] + (ko >> 1), 0, 0, 0);
-    // scales of this wave's 32 columns (lanes 32-63 repeat them), as the
-    // aligned words holding them
-    const int si = scale_index(itile.kb_code, min(itile.nb + wn + r, itile.N - 1), kb);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + kDA + kDB + wid * 256), 4,
+    for (int i = 0; i < R::WL; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + R::A + ((BN / 4) * wid + 8 * i) * 128),
+                                               16, wo[i] + (ko >> 1), 0, 0, 0);
+    // scales of this wave's BN / 2 columns (with BN 64, lanes 32-63 repeat
+    // them), as the aligned words holding them
+    const int si = scale_index(itile.kb_code, min(itile.nb + wn + scol, itile.N - 1), kb);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + R::A + R::B + wid * 256), 4,
                                              ((uint32_t)si * (uint32_t)sizeof(ScaleT)) & ~3u, 0, 0, 0);
   };
   auto advance = [&]() {
@@ -390,7 +409,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     } else if (it + 1 < my_tiles) {
       ++it;
       ikb = 0;
-      itile = dma_tile(g, xc, j + it * P, tiles_m, S, KB);
+      itile = dma_tile<BN>(g, xc, j + it * P, tiles_m, S, KB);
       bind();
     }
   };
@@ -403,68 +422,118 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
 
   // compute cursor
   int ckb = 0, ct = 0;
-  DmaTile ctile = dma_tile(g, xc, j, tiles_m, S, KB);
-  v16f acc;
+  DmaTile ctile = dma_tile<BN>(g, xc, j, tiles_m, S, KB);
+  v16f acc[NJ];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  const int arow = wm + r, brow = wn + r;
+  for (int b = 0; b < NJ; ++b)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[b][e] = 0.0f;
+  const int arow = wm + r;
   int st = 0;
   for (int u = 0; u < U; ++u) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDLoads * (DS - 2)) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::LOADS * (DS - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
     issue(st == 0 ? DS - 1 : st - 1);
     advance();
-    const uint32_t sa = lds0 + st * kDStage, sbb = sa + kDA;
-    u32x4 av[8];
-    u32x2 bv[8];
+    const uint32_t sa = lds0 + st * R::STAGE, sbb = sa + R::A;
+    v16f t[NJ];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      av[kk] = ds_read16(sa + arow * 256 + (((2 * kk + h) ^ (arow & 15)) << 4));
-      bv[kk] = ds_read8(sbb + brow * 128 + ((kk ^ ((brow >> 1) & 7)) << 4) + 8 * h);
-    }
-    uint32_t sw = ds_read4(sbb + kDB + wid * 256 + r * 4);
-    v16f t;
+    for (int b = 0; b < NJ; ++b)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) t[e] = 0.0f;
-    // each step waits only for its own two operand reads
+      for (int e = 0; e < 16; ++e) t[b][e] = 0.0f;
+    uint32_t sw[NJ];
+    if constexpr (NJ == 1) {
+      const int brow = wn + r;
+      u32x4 av[8];
+      u32x2 bv[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        av[kk] = ds_read16(sa + arow * 256 + (((2 * kk + h) ^ (arow & 15)) << 4));
+        bv[kk] = ds_read8(sbb + brow * 128 + ((kk ^ ((brow >> 1) & 7)) << 4) + 8 * h);
+      }
+      sw[0] = ds_read4(sbb + R::B + wid * 256 + r * 4);
+      // each step waits only for its own two operand reads
 #define QH_DMA_STEP(kk)                                                                   \
   lds_wait<15 - 2 * (kk)>(av[kk], bv[kk]);                                                \
-  t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),          \
-                                              e4m3x8_bf16(bv[kk]), t, 0, 0, 0);           \
+  t[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),       \
+                                                 e4m3x8_bf16(bv[kk]), t[0], 0, 0, 0);     \
   __builtin_amdgcn_sched_barrier(0);
-    QH_DMA_STEP(0) QH_DMA_STEP(1) QH_DMA_STEP(2) QH_DMA_STEP(3)
-    QH_DMA_STEP(4) QH_DMA_STEP(5) QH_DMA_STEP(6) QH_DMA_STEP(7)
+      QH_DMA_STEP(0) QH_DMA_STEP(1) QH_DMA_STEP(2) QH_DMA_STEP(3)
+      QH_DMA_STEP(4) QH_DMA_STEP(5) QH_DMA_STEP(6) QH_DMA_STEP(7)
 #undef QH_DMA_STEP
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw) : : "memory");
-    float scale;
-    if constexpr (sizeof(ScaleT) == 4) {
-      scale = __uint_as_float(sw);
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]) : : "memory");
     } else {
-      const int idx = scale_index(ctile.kb_code, min(ctile.nb + wn + r, ctile.N - 1), ctile.kb0 + ckb);
-      scale = (idx & 1) ? bf_hi(sw) : bf_lo(sw);
+      // Two 32-column tiles share each activation read.  Weights as 16-byte
+      // reads: lane half h holds chunk 2 j + h of its row and feeds half p to
+      // step 2 j + p; the activation operand is read in the same K order
+      // (bf16 chunk 4 j + 2 h + p), so both sides of a step see equal K.
+      u32x4 av[8], bq[2][4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int brow = wn + 32 * b + r;
+          bq[b][jj] = ds_read16(sbb + brow * 128 + (((2 * jj + h) ^ ((brow >> 1) & 7)) << 4));
+        }
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          av[2 * jj + p] = ds_read16(sa + arow * 256 + (((4 * jj + 2 * h + p) ^ (arow & 15)) << 4));
+      }
+      sw[0] = ds_read4(sbb + R::B + wid * 256 + r * 4);
+      sw[1] = ds_read4(sbb + R::B + wid * 256 + (32 + r) * 4);
+      // step kk waits for the reads of chunk pair kk / 2 and its activation
+#define QH_DMA_STEP2(kk)                                                                          \
+  {                                                                                               \
+    lds_wait<15 - 4 * ((kk) >> 1) - ((kk) & 1)>(av[kk], bq[0][(kk) >> 1], bq[1][(kk) >> 1]);    \
+    const v8bf a = __builtin_bit_cast(v8bf, av[kk]);                                              \
+    _Pragma("unroll") for (int b = 0; b < 2; ++b) {                                               \
+      const u32x4 wq = bq[b][(kk) >> 1];                                                          \
+      const v8bf bb = e4m3x8_bf16((kk) & 1 ? u32x2{wq.z, wq.w} : u32x2{wq.x, wq.y});              \
+      t[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb, t[b], 0, 0, 0);                       \
+    }                                                                                             \
+    __builtin_amdgcn_sched_barrier(0);                                                            \
+  }
+      QH_DMA_STEP2(0) QH_DMA_STEP2(1) QH_DMA_STEP2(2) QH_DMA_STEP2(3)
+      QH_DMA_STEP2(4) QH_DMA_STEP2(5) QH_DMA_STEP2(6) QH_DMA_STEP2(7)
+#undef QH_DMA_STEP2
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]), "+v"(sw[1]) : : "memory");
     }
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = fmaf(t[e], scale, acc[e]);
+    for (int b = 0; b < NJ; ++b) {
+      float scale;
+      if constexpr (sizeof(ScaleT) == 4) {
+        scale = __uint_as_float(sw[b]);
+      } else {
+        const int idx =
+            scale_index(ctile.kb_code, min(ctile.nb + wn + 32 * b + r, ctile.N - 1), ctile.kb0 + ckb);
+        scale = (idx & 1) ? bf_hi(sw[b]) : bf_lo(sw[b]);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[b][e] = fmaf(t[b][e], scale, acc[b][e]);
+    }
     if (++ckb == KB) {  // the item is complete: store it, start the next one
-      const int n = ctile.nb + wn + r;
       if constexpr (SPLIT) {
         float* pz = part + (size_t)(ctile.kb0 / KB) * M * ldp + ctile.tn * 64 + wn + r;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < M) pz[(size_t)m * ldp] = acc[e];
-          acc[e] = 0.0f;
+          if (m < M) pz[(size_t)m * ldp] = acc[0][e];
+          acc[0][e] = 0.0f;
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[e]);
-          acc[e] = 0.0f;
+        for (int b = 0; b < NJ; ++b) {
+          const int n = ctile.nb + wn + 32 * b + r;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[b][e]);
+            acc[b][e] = 0.0f;
+          }
         }
       }
       ckb = 0;
-      if (++ct < my_tiles) ctile = dma_tile(g, xc, j + ct * P, tiles_m, S, KB);
+      if (++ct < my_tiles) ctile = dma_tile<BN>(g, xc, j + ct * P, tiles_m, S, KB);
     }
     st = st == DS - 1 ? 0 : st + 1;
   }
@@ -480,7 +549,8 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* pa
                                                                  int ldp, GemmGroup g, int bn);
 
 // reduce = false leaves split-K partials for the caller's own finishing kernel.
-template <typename ScaleT, int DS>
+// BN = 128 is for unsplit launches.
+template <typename ScaleT, int DS, int BN = 64>
 void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, hipStream_t st,
                      int cus, int wpc, int S = 1, float* part = nullptr, bool reduce = true) {
   GemmGroup g = {};
@@ -493,7 +563,7 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
     g.N[t] = seg[t].N;
     g.kb[t] = seg[t].kb;
     g.tstart[t] = tiles_n;
-    tiles_n += (seg[t].N + 63) / 64;
+    tiles_n += (seg[t].N + BN - 1) / BN;
     const long n_scales = seg[t].kb > 1 ? (long)((seg[t].N + 127) / 128) * seg[t].kb
                           : seg[t].kb == 1 ? seg[t].N : (long)seg[t].N * (-seg[t].kb);
     // whole words: a 2-byte scale is read as the aligned word holding it
@@ -507,12 +577,19 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
   const int P = (int)max(1L, min((long)cus * wpc / 8, busiest));
   const int G = 8 * P;
   const int ldp = tiles_n * 64;
-  if (S > 1)
-    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g,
-                       M, K, tiles_n, tiles_m, S, part, ldp);
-  else
-    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false>), dim3(G), dim3(256), (size_t)DS * kDStage, st, x, g,
-                       M, K, tiles_n, tiles_m, 1, nullptr, ldp);
+  constexpr size_t lds = (size_t)DS * Ring<BN>::STAGE;
+  if constexpr (BN == 64) {
+    if (S > 1) {
+      hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true, 64>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
+                         tiles_m, S, part, ldp);
+    } else {
+      hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, 64>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
+                         tiles_m, 1, nullptr, ldp);
+    }
+  } else {
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, BN>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
+                       tiles_m, 1, nullptr, ldp);
+  }
   if (S > 1 && reduce) {
     const size_t quads = (size_t)M * ldp / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st,
@@ -724,6 +801,17 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   for (int t = 0; t < nseg; ++t)
     ring = ring && (uintptr_t)seg[t].w % 16 == 0 && (uintptr_t)seg[t].s % 4 == 0;
   if (ring) {
+    // With >= 4 64 x 128 tiles per workgroup slot (two per CU), 128-wide
+    // tiles: half the bytes per product for the same occupancy of the matrix
+    // cores (2048 x 9216 x 2560: 188 -> 132 us; at config 3a's M = 512 the
+    // 64-wide tiles' three workgroups per CU win, 40 against 44 us).
+    long tiles128 = 0;
+    for (int t = 0; t < nseg; ++t) tiles128 += (long)((seg[t].N + 127) / 128) * mt;
+    if (S == 1 && tiles128 >= 4L * cus) {
+      if (scale_bf16) launch_gemm_dma<uint16_t, 2, 128>(xa, seg, nseg, M, K, st, cus, 2);
+      else launch_gemm_dma<float, 2, 128>(xa, seg, nseg, M, K, st, cus, 2);
+      return 0;
+    }
     if (scale_bf16) launch_gemm_dma<uint16_t, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
     else launch_gemm_dma<float, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
     return 0;

@@ -569,13 +569,15 @@ def test_argmax_nan_logits_stay_in_bounds():
 # Without a workspace every shape runs the persistent ring kernel: (512, 9216,
 # 2560) and (512, 2560, 9216) are config 3a (several tiles per workgroup);
 # (5, 256, 384) an odd K-block count; (130, 200, 256), (700, 9000, 2560),
-# (2000, 4100, 384) ragged M and N (rows past M / N read as zeros).  With a
-# workspace, (128, 2560, 4096), (37, 1000, 9216) and (128, 32, 2560) split K in
-# 8, 8 and 5 (split-K kernel + reduction); the others have more tiles than
-# CUs and take the ring kernel again.
+# (2000, 4100, 384) ragged M and N (rows past M / N read as zeros).
+# (2048, 4160, 1024) and (1100, 9000, 384) have >= 1024 tiles of 64 x 128 and
+# take the 128-wide ring tiles, ragged in N (and M).  With a workspace,
+# (128, 2560, 4096), (37, 1000, 9216) and (128, 32, 2560) split K in 8, 8 and 5
+# (split-K items + reduction); the others have more tiles than CUs and take
+# the unsplit ring kernel again.
 @pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256),
-                                   (700, 9000, 2560), (2000, 4100, 384), (128, 2560, 4096),
-                                   (37, 1000, 9216), (128, 32, 2560)])
+                                   (700, 9000, 2560), (2000, 4100, 384), (2048, 4160, 1024),
+                                   (1100, 9000, 384), (128, 2560, 4096), (37, 1000, 9216), (128, 32, 2560)])
 def test_gemm_e4m3(M, N, K):
     """BASELINE config 3a: X bf16 [M, K] . deq(W)^T through the fp8 matrix cores."""
     g = gen(M + N + K)
