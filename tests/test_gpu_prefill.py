@@ -22,10 +22,14 @@ def cu(t):
     return t.to(DEV).contiguous()
 
 
-@pytest.mark.parametrize("M,past_fill", [(37, False), (70, False)])
-def test_attention_prefill(M, past_fill):
+# (tokens, past): positions 0 .. past-1 are cached by an earlier prep call,
+# positions past .. tokens-1 are the prefill.  Prefills of 256 or more tokens
+# run the matrix-core kernel (300: a ragged last 32-token block; 330 - 70 =
+# 260 after a cached prefix), shorter ones the per-token kernel.
+@pytest.mark.parametrize("M,past", [(37, 0), (70, 0), (100, 20), (256, 0), (300, 0), (330, 70)])
+def test_attention_prefill(M, past):
     g = gen(21)
-    Hq, Hkv, D, rot, max_seq = 8, 2, 256, 64, 128
+    Hq, Hkv, D, rot, max_seq = 8, 2, 256, 64, 512
     q_all = bf(randn(g, M, Hq, 2 * D))
     k, v = bf(randn(g, M, Hkv, D)), bf(randn(g, M, Hkv, D))
     qn_w, kn_w = randn(g, D, std=0.1), randn(g, D, std=0.1)
@@ -35,14 +39,17 @@ def test_attention_prefill(M, past_fill):
     q32 = torch.empty(M, Hq, D, dtype=torch.float32, device=DEV)
     kc = torch.zeros(Hkv, max_seq, D, dtype=torch.bfloat16, device=DEV)
     vc = torch.zeros_like(kc)
-    out = torch.empty(M, Hq * D, dtype=torch.bfloat16, device=DEV)
+    n = M - past
+    out = torch.empty(n, Hq * D, dtype=torch.bfloat16, device=DEV)
     dcos, dsin, dqn, dkn = cu(cos), cu(sin), cu(qn_w), cu(kn_w)
     st = abi.stream_handle()
-    abi.check(lib.qh_attn_prep(abi.ptr(dq), abi.ptr(dk_), abi.ptr(dv_), abi.ptr(dqn), abi.ptr(dkn),
-                               abi.ptr(dcos), abi.ptr(dsin), abi.ptr(q32), abi.ptr(kc), abi.ptr(vc),
-                               M, Hq, Hkv, D, rot, 0, max_seq, 1e-6, st))
-    abi.check(lib.qh_attn_prefill(abi.ptr(q32), abi.ptr(dq[:, :, D:]), Hq * 2 * D, 2 * D,
-                                  abi.ptr(kc), abi.ptr(vc), abi.ptr(out), M, Hq, Hkv, D, 0, max_seq,
+    for p0, cnt in ((0, past), (past, n)):
+        if cnt:
+            abi.check(lib.qh_attn_prep(abi.ptr(dq[p0:]), abi.ptr(dk_[p0:]), abi.ptr(dv_[p0:]), abi.ptr(dqn),
+                                       abi.ptr(dkn), abi.ptr(dcos), abi.ptr(dsin), abi.ptr(q32[p0:]),
+                                       abi.ptr(kc), abi.ptr(vc), cnt, Hq, Hkv, D, rot, p0, max_seq, 1e-6, st))
+    abi.check(lib.qh_attn_prefill(abi.ptr(q32[past:]), abi.ptr(dq[past:, :, D:]), Hq * 2 * D, 2 * D,
+                                  abi.ptr(kc), abi.ptr(vc), abi.ptr(out), n, Hq, Hkv, D, past, max_seq,
                                   st))
     torch.cuda.synchronize()
     # oracle: the attention part of OracleModel._full_prefill
@@ -64,7 +71,7 @@ def test_attention_prefill(M, past_fill):
         sc = (q[:, h] @ K[kv].t()) * (D ** -0.5) + mask
         ref[:, h] = orc.bf16(torch.softmax(sc, dim=-1) @ V[kv])
     ref = orc.bf16(ref.reshape(M, -1) * orc.bf16(torch.sigmoid(q_all[..., D:].float().reshape(M, -1))))
-    assert_close(out, ref, atol_frac=1e-3, what="prefill attention")
+    assert_close(out, ref[past:], atol_frac=1e-3, what="prefill attention")
 
 
 # M = 45: five full 8-token blocks of the scan plus a tail; M = 3: fewer
