@@ -254,14 +254,18 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint16_t* x, G
 // matrix-core step waits only for its own two operand reads.
 // LDS of one ring stage for 64 x BN tiles: X (64 rows), W (BN rows), and one
 // 64-word copy of the column scales per wave.
-template <int BN>
+// One ring stage of a BM x BN tile: X (BM rows x 128 bf16), W (BN rows x 128
+// E4M3), the BN fp32 scales (or scale words) of the block in 64-column slots.
+template <int BM, int BN>
 struct Ring {
-  static_assert(BN == 64 || BN == 128, "tile width");
-  static constexpr int A = 64 * 256;             // 64 X rows x 128 bf16
-  static constexpr int B = BN * 128;             // BN W rows x 128 E4M3
-  static constexpr int STAGE = A + B + 4 * 256;  // 25,600 B (BN 64), 33,792 B (BN 128)
+  static_assert((BM == 64 && (BN == 64 || BN == 128)) || (BM == 128 && BN == 192), "tile shape");
+  static constexpr int A = BM * 256;
+  static constexpr int B = BN * 128;
+  static constexpr int NSC = (BN + 63) / 64;     // 64-column scale slots
+  static constexpr int STAGE = A + B + NSC * 256;  // 25,088 B (64 x 64) .. 58,112 B (128 x 192)
+  static constexpr int XL = BM / 16;             // X loads (1 KB) per wave and unit
   static constexpr int WL = BN / 32;             // W loads (1 KB) per wave and unit
-  static constexpr int LOADS = 4 + WL + 1;       // per wave and unit: X, W, scales
+  static constexpr int LOADS = XL + WL + 1;      // per wave and unit: X, W, scales
 };
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -292,6 +296,14 @@ template <int N>
 __device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, u32x4& c) {
   asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a), "+v"(b), "+v"(c) : "n"(N) : "memory");
 }
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d, u32x4& e) {
+  asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e) : "n"(N) : "memory");
+}
 
 // One work item of the walk (a tile, or with split-K one K slice of a tile)
 // and its segment, all workgroup-uniform.
@@ -305,14 +317,19 @@ struct DmaTile {
 // The group is indexed in place (a kernel argument: scalar loads), never
 // copied to a local array.
 // Item i of XCD xc: K slice i % S (K blocks kb0 .. kb0 + KBs - 1) of tile
-// i / S, whose row tile is fastest.
+// i / S.  The XCD's tiles (its ntx N tiles, all row tiles) go in groups of gm
+// row tiles; within a group the row tile is fastest, so the items in flight
+// at once share gm row tiles of X and a few N tiles of W in the XCD's L2.
 template <int BN>
-__device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m, int S, int KBs) {
+__device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, int tiles_m, int S, int KBs,
+                                            int ntx, int gm) {
   DmaTile d;
   d.kb0 = (i % S) * KBs;
   i /= S;
-  d.tn = xc + 8 * (i / tiles_m);
-  d.tm = i % tiles_m;
+  const int grp = i / (gm * ntx), rr = i - grp * gm * ntx;
+  const int gme = min(gm, tiles_m - grp * gm);
+  d.tn = xc + 8 * (rr / gme);
+  d.tm = grp * gm + rr % gme;
   int si = 0;
 #pragma unroll
   for (int t = 1; t < 4; ++t)
@@ -328,28 +345,30 @@ __device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, i
 }
 
 // S > 1: each item is one K slice of a tile and its fp32 partial tile goes to
-// part[(slice M + m) ldp + global column] for gemm_splitk_reduce_kernel
-// (64-wide tiles only).  BN = 128: each wave holds two 32-column matrix-core
-// tiles that share its activation reads.
-template <typename ScaleT, int DS, bool SPLIT, int BN>
+// part[(slice M + m) ldp + global column] (ldp = tiles_n BN) for a finishing
+// kernel.  The four waves form a 2 x 2 grid of (BM / 2) x (BN / 2) sub-tiles:
+// MI x NJ 32x32 matrix-core tiles per wave, where the MI activation reads
+// and NJ weight reads of a K step are shared across them.
+template <typename ScaleT, int DS, bool SPLIT, int BN, int BM>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGroup g, int M, int K,
                                                        int tiles_n, int tiles_m, int S_arg, float* part,
-                                                       int ldp) {
-  static_assert(!SPLIT || BN == 64, "split-K uses 64-wide tiles");
-  using R = Ring<BN>;
+                                                       int ldp, int gm) {
+  using R = Ring<BM, BN>;
   constexpr int NJ = BN / 64;       // 32-column matrix-core tiles per wave
+  constexpr int MI = BM / 64;       // 32-row matrix-core tiles per wave
   const int S = SPLIT ? S_arg : 1;  // unsplit launches compile without the slice arithmetic
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
-  const int wm = (wid >> 1) * 32, wn = (wid & 1) * (BN / 2);
+  const int wm = (wid >> 1) * (BM / 2), wn = (wid & 1) * (BN / 2);
   const int KB = K / 128 / S;  // K blocks per item
   // this workgroup's items: XCD xc, its j-th of P workgroups there; XCD xc
   // owns N tiles xc, xc + 8, ... with all their row tiles (row tile fastest)
   // and K slices, dealt round-robin to its workgroups
   const int xc = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3, P = (int)gridDim.x >> 3;
-  const int ntx = tiles_n > xc ? tiles_m * ((tiles_n - xc + 7) / 8) * S : 0;
+  const int nt_x = tiles_n > xc ? (tiles_n - xc + 7) / 8 : 0;  // N tiles of this XCD
+  const int ntx = tiles_m * nt_x * S;
   const int my_tiles = j < ntx ? (ntx - j + P - 1) / P : 0;
   const int U = my_tiles * KB;
   if (U == 0) return;
@@ -358,10 +377,10 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   // lane-constant parts of the load offsets (the unit's K block is added);
   // fixed-size arrays: a lambda capturing an array whose bound depends on a
   // template parameter makes the host pass drop the kernel's launch stub
-  uint32_t xo[4], wo[4];
+  uint32_t xo[8], wo[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // X: rows 16 wid + 4 i + lane / 16
-    const int row = 16 * wid + 4 * i + (lane >> 4);
+  for (int i = 0; i < R::XL; ++i) {  // X: rows (BM / 4) wid + 4 i + lane / 16
+    const int row = (BM / 4) * wid + 4 * i + (lane >> 4);
     xo[i] = ((uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 15) ^ (row & 15)) * 8)) * 2u;
   }
 #pragma unroll
@@ -369,39 +388,53 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     const int row = (BN / 4) * wid + 8 * i + (lane >> 3);
     wo[i] = (uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) * 16);
   }
-  const int scol = lane & (BN / 2 - 1);  // this lane's scale column within the wave's
+  // scales: wave w loads the 64-column slot w % NSC (several waves may write
+  // the same slot with the same words)
+  const int sslot = wid % R::NSC, scol = 64 * sslot + lane;
 
   // issue cursor: the unit whose loads go out next (it stays on the last unit
   // once reached, so the ring keeps DS - 1 units of loads outstanding)
   int it = 0, ikb = 0;
-  DmaTile itile = dma_tile<BN>(g, xc, j, tiles_m, S, KB);
+  DmaTile itile = dma_tile<BN>(g, xc, j, tiles_m, S, KB, nt_x, gm);
   rsrc_t rx, rw, rs;
   auto bind = [&]() {
-    const int rows_m = min(M - itile.tm * 64, 64), rows_n = min(itile.N - itile.nb, BN);
-    rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x + (size_t)itile.tm * 64 * K), (short)0,
+    const int rows_m = min(M - itile.tm * BM, BM), rows_n = min(itile.N - itile.nb, BN);
+    rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x + (size_t)itile.tm * BM * K), (short)0,
                                            rows_m * K * 2, 0x00020000);
     rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(itile.w + (size_t)itile.nb * K), (short)0,
                                            rows_n * K, 0x00020000);
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(itile.s), (short)0, itile.sbytes, 0x00020000);
   };
   bind();
-  auto issue = [&](int st) {
+  // load li of the issue cursor's unit into stage st: X loads, W loads,
+  // then the scale words of the slot's 64 columns (aligned words)
+  auto issue_one = [&](int st, int li) {
     uint8_t* stage = smem + st * R::STAGE;
     const int kb = itile.kb0 + ikb;
     const uint32_t ko = (uint32_t)kb * 256u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + (16 * wid + 4 * i) * 256), 16, xo[i] + ko,
-                                               0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < R::WL; ++i)
+    if (li < R::XL) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + ((BM / 4) * wid + 4 * li) * 256), 16,
+                                               xo[li] + ko, 0, 0, 0);
+    } else if (li < R::XL + R::WL) {
+      const int i = li - R::XL;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + R::A + ((BN / 4) * wid + 8 * i) * 128),
                                                16, wo[i] + (ko >> 1), 0, 0, 0);
-    // scales of this wave's BN / 2 columns (with BN 64, lanes 32-63 repeat
-    // them), as the aligned words holding them
-    const int si = scale_index(itile.kb_code, min(itile.nb + wn + scol, itile.N - 1), kb);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + R::A + R::B + wid * 256), 4,
-                                             ((uint32_t)si * (uint32_t)sizeof(ScaleT)) & ~3u, 0, 0, 0);
+    } else {
+      const int si = scale_index(itile.kb_code, min(itile.nb + scol, itile.N - 1), kb);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(stage + R::A + R::B + sslot * 256), 4,
+                                               ((uint32_t)si * (uint32_t)sizeof(ScaleT)) & ~3u, 0, 0, 0);
+    }
+  };
+  auto issue = [&](int st) {
+#pragma unroll
+    for (int li = 0; li < R::LOADS; ++li) issue_one(st, li);
+  };
+  // the loads of step q of 8: spread over the unit's matrix-core steps so
+  // their issue overlaps the products in flight
+  auto issue_step = [&](int st, int q) {
+#pragma unroll
+    for (int li = 0; li < R::LOADS; ++li)
+      if (li * 8 / R::LOADS == q) issue_one(st, li);
   };
   auto advance = [&]() {
     if (ikb + 1 < KB) {
@@ -409,7 +442,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     } else if (it + 1 < my_tiles) {
       ++it;
       ikb = 0;
-      itile = dma_tile<BN>(g, xc, j + it * P, tiles_m, S, KB);
+      itile = dma_tile<BN>(g, xc, j + it * P, tiles_m, S, KB, nt_x, gm);
       bind();
     }
   };
@@ -422,25 +455,28 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
 
   // compute cursor
   int ckb = 0, ct = 0;
-  DmaTile ctile = dma_tile<BN>(g, xc, j, tiles_m, S, KB);
-  v16f acc[NJ];
+  DmaTile ctile = dma_tile<BN>(g, xc, j, tiles_m, S, KB, nt_x, gm);
+  v16f acc[MI][NJ];
 #pragma unroll
-  for (int b = 0; b < NJ; ++b)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[b][e] = 0.0f;
+    for (int b = 0; b < NJ; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.0f;
   const int arow = wm + r;
   int st = 0;
   for (int u = 0; u < U; ++u) {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::LOADS * (DS - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
-    issue(st == 0 ? DS - 1 : st - 1);
-    advance();
-    const uint32_t sa = lds0 + st * R::STAGE, sbb = sa + R::A;
-    v16f t[NJ];
+    const int ist = st == 0 ? DS - 1 : st - 1;  // the stage the next unit's loads fill
+    const uint32_t sa = lds0 + st * R::STAGE, sbb = sa + R::A, ssc = sbb + R::B;
+    v16f t[MI][NJ];
 #pragma unroll
-    for (int b = 0; b < NJ; ++b)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) t[b][e] = 0.0f;
+      for (int b = 0; b < NJ; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[i][b][e] = 0.0f;
     uint32_t sw[NJ];
     if constexpr (NJ == 1) {
       const int brow = wn + r;
@@ -451,53 +487,82 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
         av[kk] = ds_read16(sa + arow * 256 + (((2 * kk + h) ^ (arow & 15)) << 4));
         bv[kk] = ds_read8(sbb + brow * 128 + ((kk ^ ((brow >> 1) & 7)) << 4) + 8 * h);
       }
-      sw[0] = ds_read4(sbb + R::B + wid * 256 + r * 4);
+      sw[0] = ds_read4(ssc + (wn + r) * 4);
       // each step waits only for its own two operand reads
 #define QH_DMA_STEP(kk)                                                                   \
   lds_wait<15 - 2 * (kk)>(av[kk], bv[kk]);                                                \
-  t[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),       \
-                                                 e4m3x8_bf16(bv[kk]), t[0], 0, 0, 0);     \
+  t[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),    \
+                                                    e4m3x8_bf16(bv[kk]), t[0][0], 0, 0, 0); \
+  issue_step(ist, kk);                                                                    \
   __builtin_amdgcn_sched_barrier(0);
       QH_DMA_STEP(0) QH_DMA_STEP(1) QH_DMA_STEP(2) QH_DMA_STEP(3)
       QH_DMA_STEP(4) QH_DMA_STEP(5) QH_DMA_STEP(6) QH_DMA_STEP(7)
 #undef QH_DMA_STEP
       asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]) : : "memory");
     } else {
-      // Two 32-column tiles share each activation read.  Weights as 16-byte
-      // reads: lane half h holds chunk 2 j + h of its row and feeds half p to
-      // step 2 j + p; the activation operand is read in the same K order
-      // (bf16 chunk 4 j + 2 h + p), so both sides of a step see equal K.
-      u32x4 av[8], bq[2][4];
+      // NJ 32-column tiles share each activation read and MI row tiles each
+      // weight read.  Weights as 16-byte reads: lane half h holds chunk
+      // 2 jj + h of its row and feeds half p to step 2 jj + p; the activation
+      // operand is read in the same K order (bf16 chunk 4 jj + 2 h + p), so
+      // both sides of a step see equal K.  Reads go out in step order, per
+      // chunk pair jj: the NJ weight reads, then for p = 0, 1 the MI
+      // activation reads; LDS reads complete in order, so step kk waits until
+      // at most (total - reads through its own) are outstanding (capped at
+      // 15, the counter's limit: issue stalls while it is full).
+      constexpr int GR = NJ + 2 * MI;          // reads per chunk pair
+      constexpr int TOT = 4 * GR + NJ;         // and the scale words
+      u32x4 av[MI][8], bq[NJ][4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < NJ; ++b) {
           const int brow = wn + 32 * b + r;
           bq[b][jj] = ds_read16(sbb + brow * 128 + (((2 * jj + h) ^ ((brow >> 1) & 7)) << 4));
         }
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          av[2 * jj + p] = ds_read16(sa + arow * 256 + (((4 * jj + 2 * h + p) ^ (arow & 15)) << 4));
+#pragma unroll
+          for (int i = 0; i < MI; ++i) {
+            const int ar = arow + 32 * i;
+            av[i][2 * jj + p] = ds_read16(sa + ar * 256 + (((4 * jj + 2 * h + p) ^ (ar & 15)) << 4));
+          }
       }
-      sw[0] = ds_read4(sbb + R::B + wid * 256 + r * 4);
-      sw[1] = ds_read4(sbb + R::B + wid * 256 + (32 + r) * 4);
-      // step kk waits for the reads of chunk pair kk / 2 and its activation
-#define QH_DMA_STEP2(kk)                                                                          \
-  {                                                                                               \
-    lds_wait<15 - 4 * ((kk) >> 1) - ((kk) & 1)>(av[kk], bq[0][(kk) >> 1], bq[1][(kk) >> 1]);    \
-    const v8bf a = __builtin_bit_cast(v8bf, av[kk]);                                              \
-    _Pragma("unroll") for (int b = 0; b < 2; ++b) {                                               \
-      const u32x4 wq = bq[b][(kk) >> 1];                                                          \
-      const v8bf bb = e4m3x8_bf16((kk) & 1 ? u32x2{wq.z, wq.w} : u32x2{wq.x, wq.y});              \
-      t[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb, t[b], 0, 0, 0);                       \
-    }                                                                                             \
-    __builtin_amdgcn_sched_barrier(0);                                                            \
+#pragma unroll
+      for (int b = 0; b < NJ; ++b) sw[b] = ds_read4(ssc + (wn + 32 * b + r) * 4);
+#define QH_WAITN(kk) (TOT - ((kk) >> 1) * GR - NJ - MI * (((kk) & 1) + 1) > 15 ? 15 \
+                      : TOT - ((kk) >> 1) * GR - NJ - MI * (((kk) & 1) + 1))
+#define QH_DMA_STEPG(kk)                                                                               \
+  {                                                                                                    \
+    if constexpr (MI == 1 && NJ == 2)                                                                  \
+      lds_wait<QH_WAITN(kk)>(av[0][kk], bq[0][(kk) >> 1], bq[1][(kk) >> 1]);                          \
+    else if constexpr (MI == 2 && NJ == 2)                                                             \
+      lds_wait<QH_WAITN(kk)>(av[0][kk], av[1][kk], bq[0][(kk) >> 1], bq[1][(kk) >> 1]);               \
+    else                                                                                               \
+      lds_wait<QH_WAITN(kk)>(av[0][kk], av[MI - 1][kk], bq[0][(kk) >> 1], bq[1][(kk) >> 1],          \
+                             bq[NJ - 1][(kk) >> 1]);                                                   \
+    v8bf bb[NJ];                                                                                       \
+    _Pragma("unroll") for (int b = 0; b < NJ; ++b) {                                                   \
+      const u32x4 wq = bq[b][(kk) >> 1];                                                               \
+      bb[b] = e4m3x8_bf16((kk) & 1 ? u32x2{wq.z, wq.w} : u32x2{wq.x, wq.y});                           \
+    }                                                                                                  \
+    _Pragma("unroll") for (int i = 0; i < MI; ++i) {                                                   \
+      const v8bf a = __builtin_bit_cast(v8bf, av[i][kk]);                                              \
+      _Pragma("unroll") for (int b = 0; b < NJ; ++b)                                                   \
+        t[i][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb[b], t[i][b], 0, 0, 0);                 \
+    }                                                                                                  \
+    issue_step(ist, kk);                                                                               \
+    __builtin_amdgcn_sched_barrier(0);                                                                 \
   }
-      QH_DMA_STEP2(0) QH_DMA_STEP2(1) QH_DMA_STEP2(2) QH_DMA_STEP2(3)
-      QH_DMA_STEP2(4) QH_DMA_STEP2(5) QH_DMA_STEP2(6) QH_DMA_STEP2(7)
-#undef QH_DMA_STEP2
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]), "+v"(sw[1]) : : "memory");
+      QH_DMA_STEPG(0) QH_DMA_STEPG(1) QH_DMA_STEPG(2) QH_DMA_STEPG(3)
+      QH_DMA_STEPG(4) QH_DMA_STEPG(5) QH_DMA_STEPG(6) QH_DMA_STEPG(7)
+#undef QH_DMA_STEPG
+#undef QH_WAITN
+      if constexpr (NJ == 2)
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]), "+v"(sw[1]) : : "memory");
+      else
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]), "+v"(sw[1]), "+v"(sw[2]) : : "memory");
     }
+    advance();
 #pragma unroll
     for (int b = 0; b < NJ; ++b) {
       float scale;
@@ -509,31 +574,35 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
         scale = (idx & 1) ? bf_hi(sw[b]) : bf_lo(sw[b]);
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[b][e] = fmaf(t[b][e], scale, acc[b][e]);
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][b][e] = fmaf(t[i][b][e], scale, acc[i][b][e]);
     }
     if (++ckb == KB) {  // the item is complete: store it, start the next one
-      if constexpr (SPLIT) {
-        float* pz = part + (size_t)(ctile.kb0 / KB) * M * ldp + ctile.tn * 64 + wn + r;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (m < M) pz[(size_t)m * ldp] = acc[0][e];
-          acc[0][e] = 0.0f;
-        }
-      } else {
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int b = 0; b < NJ; ++b) {
           const int n = ctile.nb + wn + 32 * b + r;
+          if constexpr (SPLIT) {
+            float* pz = part + (size_t)(ctile.kb0 / KB) * M * ldp + ctile.tn * BN + wn + 32 * b + r;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int m = ctile.tm * 64 + wm + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[b][e]);
-            acc[b][e] = 0.0f;
+            for (int e = 0; e < 16; ++e) {
+              const int m = ctile.tm * BM + wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+              if (m < M) pz[(size_t)m * ldp] = acc[i][b][e];
+              acc[i][b][e] = 0.0f;
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int m = ctile.tm * BM + wm + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+              if (m < M && n < ctile.N) ctile.y[(size_t)m * ctile.N + n] = f2bf(acc[i][b][e]);
+              acc[i][b][e] = 0.0f;
+            }
           }
         }
-      }
       ckb = 0;
-      if (++ct < my_tiles) ctile = dma_tile<BN>(g, xc, j + ct * P, tiles_m, S, KB);
+      if (++ct < my_tiles) ctile = dma_tile<BN>(g, xc, j + ct * P, tiles_m, S, KB, nt_x, gm);
     }
     st = st == DS - 1 ? 0 : st + 1;
   }
@@ -548,9 +617,9 @@ inline bool gemm_dma_fits(int K) { return (long)64 * K * 2 < 0x7fffffffL; }
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
                                                                  int ldp, GemmGroup g, int bn);
 
-// reduce = false leaves split-K partials for the caller's own finishing kernel.
-// BN = 128 is for unsplit launches.
-template <typename ScaleT, int DS, int BN = 64>
+// reduce = false leaves split-K partials for the caller's own finishing kernel
+// (partial row stride: gemm_part_ldp).
+template <typename ScaleT, int DS, int BN, int BM>
 void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K, hipStream_t st,
                      int cus, int wpc, int S = 1, float* part = nullptr, bool reduce = true) {
   GemmGroup g = {};
@@ -569,31 +638,28 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
     // whole words: a 2-byte scale is read as the aligned word holding it
     g.sbytes[t] = (int)min((n_scales * (long)sizeof(ScaleT) + 3) & ~3L, 0x7fffffffL);
   }
-  const int tiles_m = (M + 63) / 64;
-  // P workgroups per XCD: as many as the busiest XCD has tiles (XCD 0 owns
+  const int tiles_m = (M + BM - 1) / BM;
+  // P workgroups per XCD: as many as the busiest XCD has items (XCD 0 owns
   // ceil(tiles_n / 8) N tiles), at most wpc per CU, so no workgroup there
-  // takes a second tile while others are idle
+  // takes a second item while others are idle
   const long busiest = (long)tiles_m * ((tiles_n + 7) / 8) * S;
   const int P = (int)max(1L, min((long)cus * wpc / 8, busiest));
   const int G = 8 * P;
-  const int ldp = tiles_n * 64;
-  constexpr size_t lds = (size_t)DS * Ring<BN>::STAGE;
-  if constexpr (BN == 64) {
-    if (S > 1) {
-      hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true, 64>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
-                         tiles_m, S, part, ldp);
-    } else {
-      hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, 64>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
-                         tiles_m, 1, nullptr, ldp);
-    }
+  const int ldp = tiles_n * BN;
+  // row tiles per group: about 1.5 MB of X rows (the XCD's L2 is 4 MB)
+  const int gm = (int)max(1L, min((long)tiles_m, (long)(1536 * 1024) / ((long)BM * K * 2)));
+  constexpr size_t lds = (size_t)DS * Ring<BM, BN>::STAGE;
+  if (S > 1) {
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true, BN, BM>), dim3(G), dim3(256), lds, st, x, g, M, K,
+                       tiles_n, tiles_m, S, part, ldp, gm);
   } else {
-    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, BN>), dim3(G), dim3(256), lds, st, x, g, M, K, tiles_n,
-                       tiles_m, 1, nullptr, ldp);
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, BN, BM>), dim3(G), dim3(256), lds, st, x, g, M, K,
+                       tiles_n, tiles_m, 1, nullptr, ldp, gm);
   }
   if (S > 1 && reduce) {
     const size_t quads = (size_t)M * ldp / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st,
-                       (const float*)part, S, M, ldp, g, 64);
+                       (const float*)part, S, M, ldp, g, BN);
   }
 }
 
@@ -740,9 +806,68 @@ void launch_gemm_small(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M,
 constexpr size_t kSplitPartBytes = (size_t)1024 * 64 * 64 * sizeof(float);
 
 namespace {
-// Split-K (caller workspace only) when there are no more tiles than CUs: the
-// largest S <= 8 dividing the K blocks with >= 4 blocks per slice and
-// S * tiles <= 3 per CU, so each workgroup walks fewer serial K steps.
+// Launch plan of the ring kernel: tile shape, workgroups per CU, K slices.
+struct GemmPlan {
+  int bm, bn, wpc, S;
+};
+
+// Cycles one workgroup spends per (tile, 128-wide K block) unit at its
+// occupancy (64 x 64: three workgroups per CU, 64 x 128: two, 128 x 192:
+// one), measured on MI355X at M = 512 (X fits the XCD's L2) and at M = 3700
+// (grouped row tiles; X streams): 2.0 / 2.2 / 4.3 and 2.5 / 2.6 / 3.8
+// thousand.  (128 x 128 tiles, 3.0 / 2.8 thousand, were never the fastest
+// plan for a prefill shape.)
+struct GemmShape {
+  int bm, bn, wpc;
+  double cycles_small, cycles_large;
+};
+constexpr GemmShape kGemmShapes[] = {{64, 64, 3, 2030.0, 2460.0}, {64, 128, 2, 2200.0, 2600.0},
+                                     {128, 192, 1, 4280.0, 3760.0}};
+
+// The plan with the shortest modelled time: units on the busiest XCD's
+// busiest workgroup times the unit cost, plus, when K is split (caller
+// workspace only, 2 .. 8 slices of >= 4 K blocks each), the partials'
+// round trip through memory and the finishing launch.
+GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const void* ws) {
+  const int KB = K / 128;
+  GemmPlan best = {64, 64, 3, 1};
+  double best_t = 1e300;
+  for (const GemmShape& c : kGemmShapes) {
+    long tiles_n = 0;
+    for (int t = 0; t < nseg; ++t) tiles_n += (seg[t].N + c.bn - 1) / c.bn;
+    const long tiles_m = (M + c.bm - 1) / c.bm;
+    const long slots = (long)cus * c.wpc / 8;  // workgroups per XCD
+    for (int S = 1; S <= 8; ++S) {
+      if (S > 1 && (!ws || KB % S != 0 || KB / S < 4 ||
+                    (size_t)S * M * tiles_n * c.bn * sizeof(float) > kSplitPartBytes))
+        continue;
+      const long items = tiles_m * ((tiles_n + 7) / 8) * S;
+      const long per_wg = (items + slots - 1) / slots;
+      double t = (double)per_wg * (KB / S) * (M > 1024 ? c.cycles_large : c.cycles_small);
+      if (S > 1) t += (double)S * M * tiles_n * c.bn * 4.0 * 2.0 / 2048.0 + 6000.0;
+      if (t < best_t * 0.98) {
+        best_t = t;
+        best = {c.bm, c.bn, c.wpc, S};
+      }
+    }
+  }
+  return best;
+}
+
+template <typename ScaleT>
+void launch_gemm_plan(const GemmPlan& pl, const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, int K,
+                      hipStream_t st, int cus, float* part, bool reduce) {
+  if (pl.bm == 128)
+    launch_gemm_dma<ScaleT, 2, 192, 128>(x, seg, nseg, M, K, st, cus, pl.wpc, pl.S, part, reduce);
+  else if (pl.bn == 128)
+    launch_gemm_dma<ScaleT, 2, 128, 64>(x, seg, nseg, M, K, st, cus, pl.wpc, pl.S, part, reduce);
+  else
+    launch_gemm_dma<ScaleT, 2, 64, 64>(x, seg, nseg, M, K, st, cus, pl.wpc, pl.S, part, reduce);
+}
+
+// Split-K for the per-workgroup fallback kernel (caller workspace only) when
+// there are no more tiles than CUs: the largest S <= 8 dividing the K blocks
+// with >= 4 blocks per slice and S * tiles <= 3 per CU.
 int gemm_split_count(int K, long tiles, int cus, const void* ws) {
   const int KB = K / 128;
   for (int c = 8; ws && c >= 2 && tiles <= cus; --c)
@@ -791,31 +916,21 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   // occupancy or (weights loaded straight into operand registers) the load
   // path's coalescing.
   const long tiles = tiles64 * mt;
-  const int S = gemm_split_count(K, tiles, cus, ws);
   float* part = (float*)ws;
-  // The persistent ring kernel, three workgroups per CU (two 25 KB stages
-  // each), split or not, when its direct-to-LDS loads can take the operands as
-  // they are (16-byte aligned weights, word-aligned scales, tile ranges
-  // < 2 GiB); the per-workgroup kernel otherwise.
+  // The persistent ring kernel when its direct-to-LDS loads can take the
+  // operands as they are (16-byte aligned weights, word-aligned scales, tile
+  // ranges < 2 GiB), with the modelled-fastest plan; the per-workgroup kernel
+  // otherwise.
   bool ring = gemm_dma_fits(K);
   for (int t = 0; t < nseg; ++t)
     ring = ring && (uintptr_t)seg[t].w % 16 == 0 && (uintptr_t)seg[t].s % 4 == 0;
   if (ring) {
-    // With >= 4 64 x 128 tiles per workgroup slot (two per CU), 128-wide
-    // tiles: half the bytes per product for the same occupancy of the matrix
-    // cores (2048 x 9216 x 2560: 188 -> 132 us; at config 3a's M = 512 the
-    // 64-wide tiles' three workgroups per CU win, 40 against 44 us).
-    long tiles128 = 0;
-    for (int t = 0; t < nseg; ++t) tiles128 += (long)((seg[t].N + 127) / 128) * mt;
-    if (S == 1 && tiles128 >= 4L * cus) {
-      if (scale_bf16) launch_gemm_dma<uint16_t, 2, 128>(xa, seg, nseg, M, K, st, cus, 2);
-      else launch_gemm_dma<float, 2, 128>(xa, seg, nseg, M, K, st, cus, 2);
-      return 0;
-    }
-    if (scale_bf16) launch_gemm_dma<uint16_t, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
-    else launch_gemm_dma<float, 2>(xa, seg, nseg, M, K, st, cus, 3, S, part);
+    const GemmPlan pl = gemm_plan(M, K, seg, nseg, cus, ws);
+    if (scale_bf16) launch_gemm_plan<uint16_t>(pl, xa, seg, nseg, M, K, st, cus, part, true);
+    else launch_gemm_plan<float>(pl, xa, seg, nseg, M, K, st, cus, part, true);
     return 0;
   }
+  const int S = gemm_split_count(K, tiles, cus, ws);
   if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   return 0;
@@ -838,14 +953,13 @@ int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s,
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
-    const long tiles = (long)((N + 63) / 64) * ((M + kBM - 1) / kBM);
-    const int S = gemm_split_count(K, tiles, cus, ws);
-    if (S > 1) {
-      const QhGemmSeg seg = {w, s, o, N, kb};
+    const QhGemmSeg seg = {w, s, o, N, kb};
+    const GemmPlan pl = gemm_plan(M, K, &seg, 1, cus, ws);
+    if (pl.S > 1) {
       float* part = (float*)ws;
-      if (scale_bf16) launch_gemm_dma<uint16_t, 2>((const uint16_t*)x, &seg, 1, M, K, st, cus, 3, S, part, false);
-      else launch_gemm_dma<float, 2>((const uint16_t*)x, &seg, 1, M, K, st, cus, 3, S, part, false);
-      const int ldp = ((N + 63) / 64) * 64;
+      if (scale_bf16) launch_gemm_plan<uint16_t>(pl, (const uint16_t*)x, &seg, 1, M, K, st, cus, part, false);
+      else launch_gemm_plan<float>(pl, (const uint16_t*)x, &seg, 1, M, K, st, cus, part, false);
+      const int S = pl.S, ldp = ((N + pl.bn - 1) / pl.bn) * pl.bn;
       const int v = (N / 8 + 255) / 256;
 #define QH_SAN(V)                                                                                          \
   hipLaunchKernelGGL((splitk_add_rmsnorm_kernel<V>), dim3(M), dim3(256), 0, st, (const float*)part, S, M, ldp, N, \

@@ -566,18 +566,23 @@ def test_argmax_nan_logits_stay_in_bounds():
 
 
 # ------------------------------------------------------------------ prefill GEMM
-# Without a workspace every shape runs the persistent ring kernel: (512, 9216,
-# 2560) and (512, 2560, 9216) are config 3a (several tiles per workgroup);
-# (5, 256, 384) an odd K-block count; (130, 200, 256), (700, 9000, 2560),
-# (2000, 4100, 384) ragged M and N (rows past M / N read as zeros).
-# (2048, 4160, 1024) and (1100, 9000, 384) have >= 1024 tiles of 64 x 128 and
-# take the 128-wide ring tiles, ragged in N (and M).  With a workspace,
-# (128, 2560, 4096), (37, 1000, 9216) and (128, 32, 2560) split K in 8, 8 and 5
-# (split-K items + reduction); the others have more tiles than CUs and take
-# the unsplit ring kernel again.
+# Every shape runs the persistent ring kernel, on the plan its cost model
+# picks (tile shape, workgroups per CU, K slices):
+# - (512, 9216, 2560) and (512, 2560, 9216): config 3a, 64 x 64 tiles (with a
+#   workspace the second splits K in 2);
+# - (5, 256, 384) an odd K-block count; (130, 200, 256), (2000, 4100, 384)
+#   ragged M and N (rows past M / N read as zeros);
+# - (700, 9000, 2560), (200, 12352, 384): 64 x 128 tiles; (300, 2560, 2560)
+#   with a workspace: 64 x 128 tiles, K split in 4;
+# - (1100, 9000, 384), (1500, 3000, 2560): 128 x 192 tiles, the second in
+#   groups of 2 row tiles; (2200, 1000, 4096): 64 x 64 tiles in groups of 3
+#   row tiles (35 = 11 x 3 + 2);
+# - with a workspace, (128, 2560, 4096), (37, 1000, 9216) and (128, 32, 2560)
+#   split K in 8, 8 and 5 (split-K items + reduction).
 @pytest.mark.parametrize("M,N,K", [(512, 9216, 2560), (512, 2560, 9216), (5, 256, 384), (130, 200, 256),
                                    (700, 9000, 2560), (2000, 4100, 384), (2048, 4160, 1024),
-                                   (1100, 9000, 384), (128, 2560, 4096), (37, 1000, 9216), (128, 32, 2560)])
+                                   (1100, 9000, 384), (128, 2560, 4096), (37, 1000, 9216), (128, 32, 2560),
+                                   (200, 12352, 384), (300, 2560, 2560), (1500, 3000, 2560), (2200, 1000, 4096)])
 def test_gemm_e4m3(M, N, K):
     """BASELINE config 3a: X bf16 [M, K] . deq(W)^T through the fp8 matrix cores."""
     g = gen(M + N + K)
