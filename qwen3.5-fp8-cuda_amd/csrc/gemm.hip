@@ -255,14 +255,17 @@ __global__ __launch_bounds__(256) void gemm_e4m3_lds_kernel(const uint16_t* x, G
 // LDS of one ring stage for 64 x BN tiles: X (64 rows), W (BN rows), and one
 // 64-word copy of the column scales per wave.
 // One ring stage of a BM x BN tile: X (BM rows x 128 bf16), W (BN rows x 128
-// E4M3), the BN fp32 scales (or scale words) of the block in 64-column slots.
+// E4M3), the fp32 scales (or scale words) of the block: one 64-word slot per
+// wave holding its own BN / 2 columns (BN <= 128), or three 64-column slots
+// of the tile (BN = 192).
 template <int BM, int BN>
 struct Ring {
   static_assert((BM == 64 && (BN == 64 || BN == 128)) || (BM == 128 && BN == 192), "tile shape");
   static constexpr int A = BM * 256;
   static constexpr int B = BN * 128;
-  static constexpr int NSC = (BN + 63) / 64;     // 64-column scale slots
-  static constexpr int STAGE = A + B + NSC * 256;  // 25,088 B (64 x 64) .. 58,112 B (128 x 192)
+  static constexpr bool WSLOT = BN <= 128;        // per-wave scale slots
+  static constexpr int NSC = WSLOT ? 4 : BN / 64;   // 256-byte scale slots
+  static constexpr int STAGE = A + B + NSC * 256;  // 25,600 B (64 x 64) .. 58,112 B (128 x 192)
   static constexpr int XL = BM / 16;             // X loads (1 KB) per wave and unit
   static constexpr int WL = BN / 32;             // W loads (1 KB) per wave and unit
   static constexpr int LOADS = XL + WL + 1;      // per wave and unit: X, W, scales
@@ -349,7 +352,7 @@ __device__ __forceinline__ DmaTile dma_tile(const GemmGroup& g, int xc, int i, i
 // kernel.  The four waves form a 2 x 2 grid of (BM / 2) x (BN / 2) sub-tiles:
 // MI x NJ 32x32 matrix-core tiles per wave, where the MI activation reads
 // and NJ weight reads of a K step are shared across them.
-template <typename ScaleT, int DS, bool SPLIT, int BN, int BM>
+template <typename ScaleT, int DS, bool SPLIT, int BN, int BM, bool EARLY>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGroup g, int M, int K,
                                                        int tiles_n, int tiles_m, int S_arg, float* part,
                                                        int ldp, int gm) {
@@ -388,9 +391,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     const int row = (BN / 4) * wid + 8 * i + (lane >> 3);
     wo[i] = (uint32_t)row * (uint32_t)K + (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) * 16);
   }
-  // scales: wave w loads the 64-column slot w % NSC (several waves may write
-  // the same slot with the same words)
-  const int sslot = wid % R::NSC, scol = 64 * sslot + lane;
+  // scales: per-wave slot w with the wave's BN / 2 columns (with BN 64,
+  // lanes 32-63 repeat them), or slot w % 3 of the tile's columns (two waves
+  // write slot 0 with the same words)
+  const int sslot = R::WSLOT ? wid : wid % R::NSC;
+  const int scol = R::WSLOT ? wn + (lane & (BN / 2 - 1)) : 64 * sslot + lane;
+  const int soff = R::WSLOT ? wid * 256 - wn * 4 : 0;  // LDS byte offset of column c: soff + 4 c
 
   // issue cursor: the unit whose loads go out next (it stays on the last unit
   // once reached, so the ring keeps DS - 1 units of loads outstanding)
@@ -469,6 +475,14 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::LOADS * (DS - 2)) : "memory");
     __builtin_amdgcn_s_barrier();
     const int ist = st == 0 ? DS - 1 : st - 1;  // the stage the next unit's loads fill
+    // EARLY (64 x 64 tiles): all of the next unit's loads before this unit's
+    // LDS reads, so their latency is hidden behind the whole unit; wider
+    // tiles spread them over the matrix-core steps, whose products in flight
+    // then cover the issue (3700 x 18432 x 2560: 488 -> 426 us at 128 x 192)
+    if constexpr (EARLY) {
+      issue(ist);
+      advance();
+    }
     const uint32_t sa = lds0 + st * R::STAGE, sbb = sa + R::A, ssc = sbb + R::B;
     v16f t[MI][NJ];
 #pragma unroll
@@ -487,13 +501,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
         av[kk] = ds_read16(sa + arow * 256 + (((2 * kk + h) ^ (arow & 15)) << 4));
         bv[kk] = ds_read8(sbb + brow * 128 + ((kk ^ ((brow >> 1) & 7)) << 4) + 8 * h);
       }
-      sw[0] = ds_read4(ssc + (wn + r) * 4);
+      sw[0] = ds_read4(ssc + soff + (wn + r) * 4);
       // each step waits only for its own two operand reads
 #define QH_DMA_STEP(kk)                                                                   \
   lds_wait<15 - 2 * (kk)>(av[kk], bv[kk]);                                                \
   t[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[kk]),    \
                                                     e4m3x8_bf16(bv[kk]), t[0][0], 0, 0, 0); \
-  issue_step(ist, kk);                                                                    \
+  if constexpr (!EARLY) issue_step(ist, kk);                                              \
   __builtin_amdgcn_sched_barrier(0);
       QH_DMA_STEP(0) QH_DMA_STEP(1) QH_DMA_STEP(2) QH_DMA_STEP(3)
       QH_DMA_STEP(4) QH_DMA_STEP(5) QH_DMA_STEP(6) QH_DMA_STEP(7)
@@ -528,7 +542,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
           }
       }
 #pragma unroll
-      for (int b = 0; b < NJ; ++b) sw[b] = ds_read4(ssc + (wn + 32 * b + r) * 4);
+      for (int b = 0; b < NJ; ++b) sw[b] = ds_read4(ssc + soff + (wn + 32 * b + r) * 4);
 #define QH_WAITN(kk) (TOT - ((kk) >> 1) * GR - NJ - MI * (((kk) & 1) + 1) > 15 ? 15 \
                       : TOT - ((kk) >> 1) * GR - NJ - MI * (((kk) & 1) + 1))
 #define QH_DMA_STEPG(kk)                                                                               \
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
       _Pragma("unroll") for (int b = 0; b < NJ; ++b)                                                   \
         t[i][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bb[b], t[i][b], 0, 0, 0);                 \
     }                                                                                                  \
-    issue_step(ist, kk);                                                                               \
+    if constexpr (!EARLY) issue_step(ist, kk);                                                         \
     __builtin_amdgcn_sched_barrier(0);                                                                 \
   }
       QH_DMA_STEPG(0) QH_DMA_STEPG(1) QH_DMA_STEPG(2) QH_DMA_STEPG(3)
@@ -562,7 +576,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
       else
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(sw[0]), "+v"(sw[1]), "+v"(sw[2]) : : "memory");
     }
-    advance();
+    if constexpr (!EARLY) advance();
 #pragma unroll
     for (int b = 0; b < NJ; ++b) {
       float scale;
@@ -646,16 +660,22 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
   const int P = (int)max(1L, min((long)cus * wpc / 8, busiest));
   const int G = 8 * P;
   const int ldp = tiles_n * BN;
-  // row tiles per group: about 1.5 MB of X rows (the XCD's L2 is 4 MB)
-  const int gm = (int)max(1L, min((long)tiles_m, (long)(1536 * 1024) / ((long)BM * K * 2)));
+  // row tiles per group: all of them (row tile fastest) when X fits in 3 MB
+  // of the XCD's 4 MB L2 or a workgroup takes at most two items (then the
+  // workgroups sharing a CU share X rows in its L1), else about 1.5 MB of X
+  // rows
+  const long xbytes = (long)BM * K * 2;
+  const int gm = tiles_m * xbytes <= 3L * 1024 * 1024 || busiest <= 2L * P
+                     ? tiles_m
+                     : (int)max(1L, min((long)tiles_m, (long)(1536 * 1024) / xbytes));
   constexpr size_t lds = (size_t)DS * Ring<BM, BN>::STAGE;
-  if (S > 1) {
-    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true, BN, BM>), dim3(G), dim3(256), lds, st, x, g, M, K,
-                       tiles_n, tiles_m, S, part, ldp, gm);
-  } else {
-    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, BN, BM>), dim3(G), dim3(256), lds, st, x, g, M, K,
-                       tiles_n, tiles_m, 1, nullptr, ldp, gm);
-  }
+  constexpr bool early = BM == 64 && BN == 64;
+  if (S > 1)
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, true, BN, BM, early>), dim3(G), dim3(256), lds, st, x, g, M,
+                       K, tiles_n, tiles_m, S, part, ldp, gm);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<ScaleT, DS, false, BN, BM, early>), dim3(G), dim3(256), lds, st, x, g, M,
+                       K, tiles_n, tiles_m, 1, nullptr, ldp, gm);
   if (S > 1 && reduce) {
     const size_t quads = (size_t)M * ldp / 4;
     hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st,
