@@ -78,11 +78,12 @@ def test_attention_prefill(M, past):
 # tokens than the conv window (the ring supplies them all); past > 0 with a
 # filled ring and state: the conv reads positions before the prompt.
 # algo "chunk" (qh_gdn_chunk): M = 64 one full chunk, 130 two chunks and a
-# 2-token tail, 200 from a stored state over four chunks.
+# 2-token tail, 200 from a stored state over four chunks, 600 (from a stored
+# state) the 8-channel conv kernel of prompts of 512+ tokens.
 @pytest.mark.parametrize("M,past,algo", [(45, 0, "scan"), (3, 0, "scan"), (8, 6, "scan"),
                                          (21, 6, "scan"), (45, 0, "chunk"), (3, 0, "chunk"),
                                          (21, 6, "chunk"), (64, 0, "chunk"), (130, 0, "chunk"),
-                                         (200, 6, "chunk")])
+                                         (200, 6, "chunk"), (600, 6, "chunk")])
 def test_gdn_prefill(M, past, algo):
     g = gen(22 + M + past)
     Hk, Hv, dk, dv = 2, 4, 128, 128
@@ -163,9 +164,10 @@ def test_gdn_prefill(M, past, algo):
         assert_close(state, S_c, rtol=1e-3, atol_frac=1e-4, what="final state (chunked)")
 
 
-def test_silu_mul_exact():
+# n % 8 == 0 takes the 16-byte kernel, 10007 the element kernel
+@pytest.mark.parametrize("n", [10007, 10000, 3 * 9216])
+def test_silu_mul_exact(n):
     g = gen(23)
-    n = 10007
     a, b = bf(randn(g, n)), bf(randn(g, n))
     lib = abi.load()
     da, db = cu(a), cu(b)
