@@ -350,7 +350,7 @@ int qh_gdn_scan(const void* qn, const void* kn, const void* y, const float* g, c
                 int dk, int dv, float eps, qh_stream_t stream);
 
 /* Workspace bytes of qh_gdn_chunk for M tokens and Hv value heads
- * (Hv * ceil(M / 64) * 98560). */
+ * (Hv * ceil(M / 64) * 99328). */
 size_t qh_gdn_chunk_workspace_size(int M, int Hv);
 
 /* qh_gdn_scan in the chunked (WY) form the reference's prefill uses

@@ -39,9 +39,12 @@ constexpr int NCG = DV / 16;     // state-kernel workgroups per head
 constexpr float kQScale = 0.0883883476483184405f;  // 128^-1/2
 
 // Workspace of one (head, chunk) unit, in floats: W [CH][DK], U [CH][DV],
-// Att [CH][CH] (the masked, scaled Q K^T), G [CH], K^T [DK][CH] bf16.
+// Att [CH][CH] (the masked, scaled Q K^T), G [CH], K^T [DK][CH] bf16, and the
+// decays the state kernel applies: E [CH] = e^(G_last - G), QE [CH] =
+// 128^-1/2 e^G, and e^(G_last) (padded to CH).
 constexpr size_t kW = 0, kU = (size_t)CH * DK, kAtt = kU + (size_t)CH * DV, kG = kAtt + (size_t)CH * CH,
-                 kKT = kG + CH, kUnitFloats = kKT + (size_t)DK * CH / 2;
+                 kKT = kG + CH, kE = kKT + (size_t)DK * CH / 2, kQE = kE + CH, kEL = kQE + CH,
+                 kUnitFloats = kEL + CH;
 
 typedef short bf4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -143,6 +146,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(QhGdnScanParams p, 
     }
     sG[lane] = x;
     unit[kG + lane] = x;
+    const float glast = __shfl(x, CH - 1, 64);
+    unit[kE + lane] = expf(glast - x);
+    unit[kQE + lane] = kQScale * expf(x);
+    if (lane == 0) unit[kEL] = expf(glast);
   }
   __syncthreads();
 
@@ -290,12 +297,12 @@ struct RowOps {
   u32x2 q[DK / 16];  // q[ar][16 s + kc .. +3], bf16
   f4 att[CH / 16];   // Att[ar][16 s + kc .. +3]
   float u[4];        // U[16 w + kc + r][16 cg + col]
-  float gar;         // G[ar]
+  float qe;          // 128^-1/2 e^G[ar]
 };
 struct StateOps {
   bf4 kt[2][CH / 16];    // K^T rows 16 td + col (td = 2 (w-4) + tt), tokens 16 s + kc .. +3
-  float gb[CH / 16][4];  // G[16 s + kc + r]
-  float glast;           // G[CH - 1]
+  float eb[CH / 16][4];  // e^(G_last - G[16 s + kc + r])
+  float elast;           // e^(G_last)
 };
 
 __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p, const float* ws, int nch) {
@@ -304,7 +311,15 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
   constexpr int SST = DK + 4, VST = CH + 4;
   __shared__ __align__(16) float sS[16 * SST];   // the state slice, sS[column][d]
   __shared__ __align__(16) float sVn[16 * VST];  // V' of the chunk, sVn[column][token]
-  const int h = blockIdx.x / NCG, cg = blockIdx.x % NCG, kh = h / (p.Hv / p.Hk);
+  // The NCG workgroups of a head share its chunk operands (W, Att, q, K^T):
+  // with Hv % 8 == 0 they are placed on one XCD (workgroup i runs on XCD
+  // i % 8), so those operands come from memory once per head, not once per
+  // column group.
+  const int bid = (int)blockIdx.x;
+  const bool xcd = p.Hv % 8 == 0;
+  const int h = xcd ? ((bid >> 3) / NCG) * 8 + (bid & 7) : bid / NCG;
+  const int cg = xcd ? (bid >> 3) % NCG : bid % NCG;
+  const int kh = h / (p.Hv / p.Hk);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, kc = 4 * (lane >> 4);
   float* state = p.state + (size_t)h * DK * DV + cg * 16;
@@ -315,6 +330,11 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
   if (w < 4) {
     // ---------------------------------------------------------- row waves
     const int ar = 16 * w + col;  // A-operand row (token) of this lane
+    // the workgroup's 16 output columns of every token (a uniform resource;
+    // the lane's column goes in the offset): bytes past row M - 1 are out of
+    // the resource's range
+    const auto rout = __builtin_amdgcn_make_buffer_rsrc(p.out + (size_t)h * DV + cg * 16, (short)0,
+                                                        (int)(((size_t)(p.M - 1) * p.Hv * DV + 16) * 2), 0x00020000);
     auto load = [&](RowOps& o, int c) {
       const float* unit = units + (size_t)c * kUnitFloats;
       const int t = min(c * CH + ar, p.M - 1);  // rows past M: any row (outputs dropped)
@@ -328,7 +348,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
       for (int s = 0; s < CH / 16; ++s) o.att[s] = *(const f4*)(unit + kAtt + ar * CH + 16 * s + kc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) o.u[r] = unit[kU + (size_t)(16 * w + kc + r) * DV + cg * 16 + col];
-      o.gar = unit[kG + ar];
+      o.qe = unit[kQE + ar];
     };
     auto step = [&](const RowOps& cur, int c) {
       const int t0 = c * CH;
@@ -339,7 +359,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
         Sv = *(const f4*)(sS + col * SST + 16 * s + kc);
         split4(Sv, Sh[s], Sl[s]);
       }
-      const float qs = kQScale * expf(cur.gar);
+      const float qs = cur.qe;
       f4 ws_acc = zero4(), o = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 16; ++s) {
@@ -368,10 +388,13 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
         o = mma(ah, vl, o);
         o = mma(al, vh, o);
       }
+      // range-checked stores: rows past M are dropped without a branch (a
+      // guarded store in this loop made the compiler wait for every
+      // outstanding load, the next chunk's operands included, at its head)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * w + kc + r;
-        if (t0 + i < p.M) p.out[(size_t)(t0 + i) * p.Hv * DV + (size_t)h * DV + cg * 16 + col] = f2bf(o[r]);
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(o[r]), rout, (uint32_t)(((t0 + i) * p.Hv * DV + col) * 2), 0, 0);
       }
       __syncthreads();  // V' read; the new state written
     };
@@ -398,20 +421,20 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
 #pragma unroll
       for (int s = 0; s < CH / 16; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o.gb[s][r] = unit[kG + 16 * s + kc + r];
-      o.glast = unit[kG + CH - 1];
+        for (int r = 0; r < 4; ++r) o.eb[s][r] = unit[kE + 16 * s + kc + r];
+      o.elast = unit[kEL];
     };
     // S <- e^{G_last} S + K^T diag(e^{G_last - G}) V', d tiles 2 sw, 2 sw + 1
     auto step = [&](const StateOps& cur) {
       __syncthreads();  // V' complete
-      const float gl = cur.glast, eg = expf(gl);
+      const float eg = cur.elast;
       bf4 Bh[CH / 16], Bl[CH / 16];
 #pragma unroll
       for (int s = 0; s < CH / 16; ++s) {
         const f4 v = *(const f4*)(sVn + col * VST + 16 * s + kc);
         f4 x;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = expf(gl - cur.gb[s][r]) * v[r];
+        for (int r = 0; r < 4; ++r) x[r] = cur.eb[s][r] * v[r];
         split4(x, Bh[s], Bl[s]);
       }
 #pragma unroll

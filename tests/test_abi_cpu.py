@@ -106,7 +106,7 @@ def test_validation_errors_need_no_gpu():
                           1e-6, None, 0, None)
     assert rc == -1 and "unsupported shape" in abi.last_error()
     need = int(lib.qh_gdn_chunk_workspace_size(130, 32))
-    assert need == 32 * 3 * 98560
+    assert need == 32 * 3 * 99328
     rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, 16, 32, 128, 128,
                           1e-6, None, need, None)
     assert rc == -1 and "workspace" in abi.last_error()

@@ -118,7 +118,7 @@ def test_gdn_prefill(M, past, algo):
                                   dk, dv, 1e-6, st))
     else:
         nws = int(lib.qh_gdn_chunk_workspace_size(M, Hv))
-        assert nws == Hv * ((M + 63) // 64) * 98560
+        assert nws == Hv * ((M + 63) // 64) * 99328
         ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
         abi.check(lib.qh_gdn_chunk(abi.ptr(qn), abi.ptr(kn), abi.ptr(y), abi.ptr(gg), abi.ptr(beta),
                                    abi.ptr(dz), abi.ptr(dnw), abi.ptr(state), abi.ptr(out), M, Hk, Hv,
