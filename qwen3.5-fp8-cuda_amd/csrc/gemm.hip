@@ -847,7 +847,10 @@ constexpr GemmShape kGemmShapes[] = {{64, 64, 3, 2030.0, 2460.0}, {64, 128, 2, 2
 // The plan with the shortest modelled time: units on the busiest XCD's
 // busiest workgroup times the unit cost, plus, when K is split (caller
 // workspace only, 2 .. 8 slices of >= 4 K blocks each), the partials'
-// round trip through memory and the finishing launch.
+// round trip through memory and the finishing launch (≈ 6 us: 128 x 10240 x
+// 2560 took 17.7 us unsplit and 21.9 us in two slices).  Deeper rings for
+// 64 x 64 tiles (three or four stages, fewer workgroups per CU) measured no
+// faster at M = 128 and 512.
 GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const void* ws) {
   const int KB = K / 128;
   GemmPlan best = {64, 64, 3, 1};
@@ -864,7 +867,7 @@ GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const 
       const long items = tiles_m * ((tiles_n + 7) / 8) * S;
       const long per_wg = (items + slots - 1) / slots;
       double t = (double)per_wg * (KB / S) * (M > 1024 ? c.cycles_large : c.cycles_small);
-      if (S > 1) t += (double)S * M * tiles_n * c.bn * 4.0 * 2.0 / 2048.0 + 6000.0;
+      if (S > 1) t += (double)S * M * tiles_n * c.bn * 4.0 * 2.0 / 2048.0 + 13000.0;
       if (t < best_t * 0.98) {
         best_t = t;
         best = {c.bm, c.bn, c.wpc, S};
