@@ -38,7 +38,7 @@ constexpr int AS = 68;           // fp32 row stride of A
 constexpr int NCG = DV / 16;     // state-kernel workgroups per head
 constexpr float kQScale = 0.0883883476483184405f;  // 128^-1/2
 
-// Workspace of one (head, chunk) unit, in floats: W [CH][DK], U [CH][DV],
+// Workspace of one (head, chunk) unit, in floats: W [CH][DK], U^T [DV][CH],
 // Att [CH][CH] (the masked, scaled Q K^T), G [CH], K^T [DK][CH] bf16, and the
 // decays the state kernel applies: E [CH] = e^(G_last - G), QE [CH] =
 // 128^-1/2 e^G, and e^(G_last) (padded to CH).
@@ -269,11 +269,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(QhGdnScanParams p, 
     }
 #pragma unroll
     for (int tn = 0; tn < DK / 16; ++tn) {
+      // U transposed: a lane's 4 tokens of one column are one 16-byte store
+      // here and one 16-byte load in the state kernel
+      *(f4*)(unit + kU + (size_t)(16 * tn + (lane & 15)) * CH + 16 * w + kc) = ua[tn];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * w + kc + r, d = 16 * tn + (lane & 15);
         unit[kW + i * DK + d] = wa[tn][r];
-        unit[kU + i * DV + d] = ua[tn][r];
       }
     }
   }
@@ -296,12 +298,12 @@ struct RowOps {
   f4 w[DK / 16];     // W[ar][16 s + kc .. +3]
   u32x2 q[DK / 16];  // q[ar][16 s + kc .. +3], bf16
   f4 att[CH / 16];   // Att[ar][16 s + kc .. +3]
-  float u[4];        // U[16 w + kc + r][16 cg + col]
+  f4 u;              // U[16 w + kc + r][16 cg + col], r = 0..3
   float qe;          // 128^-1/2 e^G[ar]
 };
 struct StateOps {
   bf4 kt[2][CH / 16];    // K^T rows 16 td + col (td = 2 (w-4) + tt), tokens 16 s + kc .. +3
-  float eb[CH / 16][4];  // e^(G_last - G[16 s + kc + r])
+  f4 eb[CH / 16];        // e^(G_last - G[16 s + kc + r])
   float elast;           // e^(G_last)
 };
 
@@ -346,8 +348,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
       }
 #pragma unroll
       for (int s = 0; s < CH / 16; ++s) o.att[s] = *(const f4*)(unit + kAtt + ar * CH + 16 * s + kc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o.u[r] = unit[kU + (size_t)(16 * w + kc + r) * DV + cg * 16 + col];
+      o.u = *(const f4*)(unit + kU + (size_t)(cg * 16 + col) * CH + 16 * w + kc);
       o.qe = unit[kQE + ar];
     };
     auto step = [&](const RowOps& cur, int c) {
@@ -398,13 +399,18 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
       }
       __syncthreads();  // V' read; the new state written
     };
+    // the next chunk's loads go out before the step (a scheduling barrier
+    // keeps the compiler from sinking them into it, where the next step's
+    // wait would expose their latency)
     RowOps ra, rb;
     load(ra, 0);
     for (int c = 0; c < nch; c += 2) {
       load(rb, min(c + 1, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
       step(ra, c);
       if (c + 1 >= nch) break;
       load(ra, min(c + 2, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
       step(rb, c + 1);
     }
   } else {
@@ -418,10 +424,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
 #pragma unroll
         for (int s = 0; s < CH / 16; ++s)
           o.kt[tt][s] = *(const bf4*)(kt + (16 * (2 * sw + tt) + col) * CH + 16 * s + kc);
+      // one 16-byte load per 4 decays: the loads' count, not their bytes,
+      // is what the chunk loop's issue waits on
 #pragma unroll
-      for (int s = 0; s < CH / 16; ++s)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o.eb[s][r] = unit[kE + 16 * s + kc + r];
+      for (int s = 0; s < CH / 16; ++s) o.eb[s] = *(const f4*)(unit + kE + 16 * s + kc);
       o.elast = unit[kEL];
     };
     // S <- e^{G_last} S + K^T diag(e^{G_last - G}) V', d tiles 2 sw, 2 sw + 1
@@ -454,9 +460,11 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
     load(sa, 0);
     for (int c = 0; c < nch; c += 2) {
       load(sb, min(c + 1, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
       step(sa);
       if (c + 1 >= nch) break;
       load(sa, min(c + 2, nch - 1));
+      __builtin_amdgcn_sched_barrier(0);
       step(sb);
     }
   }
