@@ -18,16 +18,19 @@
 // enables split-K (qh_gemm_e4m3 / qh_gemm_e4m3_grouped).  The reference entry
 // point fp8_gemm_batch passes none and never splits.
 //
-// Two kernels, both on 64 x 64 output tiles (a 2 x 2 grid of waves, each one
-// 32x32 matrix-core tile) in an XCD-aware tile order (the row tiles of one
-// weight tile run on one XCD and share it in that XCD's L2):
+// Two kernels, both with a 2 x 2 grid of waves per output tile in an
+// XCD-aware tile order (the row tiles of one weight tile run on one XCD and
+// share it in that XCD's L2):
 //  - gemm_dma_kernel (every launch whose operands it can take): persistent
-//    workgroups, three per CU, stream (tile or tile K slice, K block) units
-//    through a two-stage LDS ring filled by direct-to-LDS loads; split-K
-//    partials are finished by gemm_splitk_reduce_kernel;
+//    workgroups stream (tile or tile K slice, K block) units through a
+//    two-stage LDS ring filled by direct-to-LDS loads, on 64 x 64 tiles
+//    (three workgroups per CU), 64 x 128 (two) or 128 x 192 (one), the plan
+//    (tile shape, K split) picked by a cost model with measured per-unit
+//    cycles (gemm_plan); split-K partials are finished by
+//    gemm_splitk_reduce_kernel or splitk_add_rmsnorm_kernel;
 //  - gemm_e4m3_lds_kernel (fallback for unaligned weights or scales): one
-//    workgroup per (tile, K slice), the next K blocks in registers while the
-//    current one is multiplied.
+//    workgroup per (64 x 64 tile, K slice), the next K blocks in registers
+//    while the current one is multiplied.
 // Operand layout of the 32x32x16 bf16 instruction (measured on gfx950):
 // lane l holds A[l % 32][8 (l / 32) + r] and B[8 (l / 32) + r][l % 32],
 // r = 0..7, and accumulator value e is C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
@@ -711,12 +714,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* pa
 //   o = bf16(sum_z part[z][m][:N])  (z in order, as gemm_splitk_reduce_kernel),
 //   h = bf16(h + o) in place, hn = bf16(h * rsqrt(mean(h^2) + eps) * (1 + w))
 // (no hn when w is null).  V 8-column vectors per thread stay in registers;
-// requires N % 8 == 0, N <= 2048 V and 16-byte aligned rows.
-template <int V>
-__global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* part, int S, int M, int ldp, int N,
+// requires N % 8 == 0, N <= 2048 V and 16-byte aligned rows.  SC > 0: the
+// slice count as a constant, so all of a vector's partial loads are in flight
+// at once (with a runtime count the loop issued them one round trip apart).
+template <int V, int SC>
+__global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* part, int S_arg, int M, int ldp, int N,
                                                                  uint16_t* h, const float* w, uint16_t* hn,
                                                                  float eps) {
   __shared__ float red[4];
+  const int S = SC > 0 ? SC : S_arg;
   const int m = blockIdx.x, t = threadIdx.x, nv = N >> 3;
   uint16_t* hr = h + (size_t)m * N;
   float xv[V][8];
@@ -727,6 +733,7 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* pa
     if (i < nv) {
       const float* p0 = part + (size_t)m * ldp + 8 * i;
       f32x4 a0 = *(const f32x4*)p0, a1 = *(const f32x4*)(p0 + 4);
+#pragma unroll
       for (int z = 1; z < S; ++z) {
         const float* pz = p0 + (size_t)z * M * ldp;
         a0 += *(const f32x4*)pz;
@@ -984,12 +991,20 @@ int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s,
       else launch_gemm_plan<float>(pl, (const uint16_t*)x, &seg, 1, M, K, st, cus, part, false);
       const int S = pl.S, ldp = ((N + pl.bn - 1) / pl.bn) * pl.bn;
       const int v = (N / 8 + 255) / 256;
-#define QH_SAN(V)                                                                                          \
-  hipLaunchKernelGGL((splitk_add_rmsnorm_kernel<V>), dim3(M), dim3(256), 0, st, (const float*)part, S, M, ldp, N, \
+#define QH_SAN(V, SC)                                                                                          \
+  hipLaunchKernelGGL((splitk_add_rmsnorm_kernel<V, SC>), dim3(M), dim3(256), 0, st, (const float*)part, S, M, ldp, N, \
                      (uint16_t*)h, norm_w, (uint16_t*)hn, eps)
-      if (v <= 1) QH_SAN(1);
-      else if (v == 2) QH_SAN(2);
-      else QH_SAN(4);
+#define QH_SAN_S(V)             \
+  switch (S) {                  \
+    case 2: QH_SAN(V, 2); break; \
+    case 4: QH_SAN(V, 4); break; \
+    case 8: QH_SAN(V, 8); break; \
+    default: QH_SAN(V, 0); break; \
+  }
+      if (v <= 1) QH_SAN_S(1)
+      else if (v == 2) QH_SAN_S(2)
+      else QH_SAN_S(4)
+#undef QH_SAN_S
 #undef QH_SAN
       return 0;
     }
