@@ -686,6 +686,18 @@ void launch_gemm_dma(const uint16_t* x, const QhGemmSeg* seg, int nseg, int M, i
   }
 }
 
+// sum_z p[z zs] (four floats), z in order, every load issued first
+template <int S>
+__device__ __forceinline__ f32x4 sum_slices(const float* p, size_t zs) {
+  f32x4 a[S];
+#pragma unroll
+  for (int z = 0; z < S; ++z) a[z] = *(const f32x4*)(p + z * zs);
+  f32x4 acc = a[0];
+#pragma unroll
+  for (int z = 1; z < S; ++z) acc += a[z];
+  return acc;
+}
+
 // Split-K finish: y = bf16(sum_z part[z][m][column]), summed in z order;
 // columns past a segment's N (tile padding) are skipped.  Four columns per
 // thread (segments start at multiples of 64 columns).
@@ -701,8 +713,23 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* pa
     if (t < g.nseg && tile >= g.tstart[t]) si = t;
   const int n = ng - g.tstart[si] * bn, N = g.N[si];
   if (n >= N) return;
-  f32x4 acc = *(const f32x4*)(part + (size_t)m * ldp + ng);
-  for (int z = 1; z < S; ++z) acc += *(const f32x4*)(part + ((size_t)z * M + m) * ldp + ng);
+  // the slices' loads all in flight (a runtime-count loop issued them one
+  // round trip apart), summed in slice order
+  const float* p = part + (size_t)m * ldp + ng;
+  const size_t zs = (size_t)M * ldp;
+  f32x4 acc;
+  switch (S) {
+    case 2: acc = sum_slices<2>(p, zs); break;
+    case 3: acc = sum_slices<3>(p, zs); break;
+    case 4: acc = sum_slices<4>(p, zs); break;
+    case 5: acc = sum_slices<5>(p, zs); break;
+    case 6: acc = sum_slices<6>(p, zs); break;
+    case 7: acc = sum_slices<7>(p, zs); break;
+    case 8: acc = sum_slices<8>(p, zs); break;
+    default:
+      acc = *(const f32x4*)p;
+      for (int z = 1; z < S; ++z) acc += *(const f32x4*)(p + z * zs);
+  }
   uint16_t* y = g.y[si] + (size_t)m * N + n;
 #pragma unroll
   for (int c = 0; c < 4; ++c)
