@@ -105,27 +105,46 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(QhGdnScanParams p, 
   const int t0 = c * CH;
   float* unit = ws + ((size_t)h * nch + c) * kUnitFloats;
 
-  // ---- the chunk's K, Q (token-major) and K, V (dim-major); rows past M are 0
-  for (int e = tid; e < CH * (DK / 8); e += 256) {
-    const int i = e >> 4, c8 = (e & 15) * 8;
-    const bool ok = t0 + i < p.M;
-    const int t = ok ? t0 + i : p.M - 1;
+  // ---- the chunk's K, Q (token-major) and K, V (dim-major); rows past M are 0.
+  // Waves 0-1 take K, waves 2-3 V: a thread holds 8 tokens x 8 dims, stores
+  // them token-major (K) and, transposed in registers (v_perm), as 16-byte
+  // rows of the dim-major tile (2-byte scatter stores hit 8-way LDS bank
+  // conflicts); every thread also copies 4 16-byte pieces of Q.
+  {
     const u32x4 zero = {0u, 0u, 0u, 0u};
-    u32x4 kq = *(const u32x4*)(p.kn + ((size_t)t * p.Hk + kh) * DK + c8);
-    u32x4 qq = *(const u32x4*)(p.qn + ((size_t)t * p.Hk + kh) * DK + c8);
-    u32x4 vq = *(const u32x4*)(p.y + (size_t)t * p.C + (size_t)2 * p.Hk * DK + (size_t)h * DV + c8);
-    kq = ok ? kq : zero;
-    qq = ok ? qq : zero;
-    vq = ok ? vq : zero;
-    *(u32x4*)(sK + i * RS + c8) = kq;
-    *(u32x4*)(sQ + i * RS + c8) = qq;
-    const uint32_t kw[4] = {kq.x, kq.y, kq.z, kq.w}, vw[4] = {vq.x, vq.y, vq.z, vq.w};
+    const bool is_v = tid >= 128;  // wave-uniform
+    const int tt = tid & 127, tg = tt & 7, dg = tt >> 3;  // tokens 8 tg .. + 7, dims 8 dg .. + 7
+    u32x4 x[8], qv[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      sKT[(c8 + 2 * u) * TS + i] = (uint16_t)(kw[u] & 0xFFFFu);
-      sKT[(c8 + 2 * u + 1) * TS + i] = (uint16_t)(kw[u] >> 16);
-      sVT[(c8 + 2 * u) * TS + i] = (uint16_t)(vw[u] & 0xFFFFu);
-      sVT[(c8 + 2 * u + 1) * TS + i] = (uint16_t)(vw[u] >> 16);
+    for (int j = 0; j < 8; ++j) {
+      const int t = min(t0 + 8 * tg + j, p.M - 1);
+      x[j] = is_v ? *(const u32x4*)(p.y + (size_t)t * p.C + (size_t)2 * p.Hk * DK + (size_t)h * DV + 8 * dg)
+                  : *(const u32x4*)(p.kn + ((size_t)t * p.Hk + kh) * DK + 8 * dg);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = tid + 256 * r, i = e >> 4, c8 = (e & 15) * 8;
+      qv[r] = *(const u32x4*)(p.qn + ((size_t)min(t0 + i, p.M - 1) * p.Hk + kh) * DK + c8);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = 8 * tg + j;
+      if (t0 + i >= p.M) x[j] = zero;
+      if (!is_v) *(u32x4*)(sK + i * RS + 8 * dg) = x[j];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = tid + 256 * r, i = e >> 4, c8 = (e & 15) * 8;
+      *(u32x4*)(sQ + i * RS + c8) = t0 + i < p.M ? qv[r] : zero;
+    }
+    uint16_t* dT = is_v ? sVT : sKT;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // dim 8 dg + j: tokens 8 tg .. + 7, pairs of 16-bit halves
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      u32x4 col;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) col[q] = __builtin_amdgcn_perm(x[2 * q + 1][j >> 1], x[2 * q][j >> 1], sel);
+      *(u32x4*)(dT + (8 * dg + j) * TS + 8 * tg) = col;
     }
   }
   if (tid < CH) {
