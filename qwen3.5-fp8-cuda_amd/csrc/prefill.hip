@@ -634,6 +634,20 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(QhGdnScanParams p) {
 
 // ---- gated RMSNorm of the scan output, in place: one 128-thread block per
 // (token, head) (main.py:1152-1158) --------------------------------------------
+// One wave per (token, head), four per block, no LDS or barrier: lane j
+// holds elements j and j + 64 and the two 64-element sums are added as the
+// two-wave kernel below does, so the results are the same bit for bit.
+__global__ __launch_bounds__(256) void gdn_gated_norm_wave_kernel(QhGdnScanParams p) {
+  const int idx = (int)blockIdx.x * 4 + (threadIdx.x >> 6), j = threadIdx.x & 63;
+  if (idx >= p.M * p.Hv) return;
+  const size_t o = (size_t)idx * 128 + j;  // token idx / Hv, head idx % Hv: rows of Hv * 128
+  const float c0 = bf2f(p.out[o]), c1 = bf2f(p.out[o + 64]);
+  const float z0 = bf2f(p.z[o]), z1 = bf2f(p.z[o + 64]);
+  const float w0 = bf2f(p.norm_w[j]), w1 = bf2f(p.norm_w[j + 64]);
+  const float rs = rsqrtf((wave_sum(c0 * c0) + wave_sum(c1 * c1)) / 128.0f + p.eps);
+  p.out[o] = f2bf(rbf(rbf(c0 * rs) * w0) * rbf(qh_silu(z0)));
+  p.out[o + 64] = f2bf(rbf(rbf(c1 * rs) * w1) * rbf(qh_silu(z1)));
+}
 __global__ __launch_bounds__(128) void gdn_gated_norm_kernel(QhGdnScanParams p) {
   __shared__ float red2[2];
   const int m = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
@@ -808,7 +822,12 @@ int qh_launch_gdn_scan(const QhGdnScanParams& p, hipStream_t st) {
 
 int qh_launch_gdn_gated_norm(const QhGdnScanParams& p, hipStream_t st) {
   if (p.M <= 0) return 0;
-  hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(p.M, p.Hv), dim3(128), 0, st, p);
+  if (p.dv == 128) {
+    const long n = (long)p.M * p.Hv;
+    hipLaunchKernelGGL(gdn_gated_norm_wave_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(p.M, p.Hv), dim3(128), 0, st, p);
+  }
   return 0;
 }
 
