@@ -502,13 +502,23 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(QhGdnPrepParams p) {
 // row computes the Hv gates of token m.
 // The blocks of token 0 also store the ring's last four positions (slot
 // (past + m) % 4 holds x of token m), once the conv has read it.
-__global__ __launch_bounds__(64) void gdn_norm_gates_kernel(QhGdnPrepParams p) {
-  const int m = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
-  if (m == 0) {
-    const int nthr = gridDim.y * 64;
-    for (int c = row * 64 + lane; c < p.C; c += nthr)
-      for (int t = max(0, p.M - 4); t < p.M; ++t)
-        p.conv_ring[(size_t)c * 4 + ((p.past + t) & 3)] = p.mixed[(size_t)t * p.C + c];
+// Four (token, row) waves per 256-thread block (row < 2 Hk: the l2norm of a
+// q or k head; row 2 Hk: the gates), each wave as the one-wave blocks it
+// replaced.  Every thread of the grid also stores its share of the conv
+// ring's last four positions (one (channel, position) copy per thread from
+// 16 tokens; token 0's waves alone made one memory round trip per copy).
+__global__ __launch_bounds__(256) void gdn_norm_gates_kernel(QhGdnPrepParams p) {
+  const int rows = 2 * p.Hk + 1;
+  const int idx = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (idx >= p.M * rows) return;
+  const int m = idx / rows, row = idx - m * rows;
+  {
+    const int nt = min(4, p.M);
+    const long total = (long)p.C * nt, nthr = (long)p.M * rows * 64;
+    for (long it = (long)idx * 64 + lane; it < total; it += nthr) {
+      const int c = (int)(it / nt), t = p.M - nt + (int)(it - (long)c * nt);
+      p.conv_ring[(size_t)c * 4 + ((p.past + t) & 3)] = p.mixed[(size_t)t * p.C + c];
+    }
   }
   if (row < 2 * p.Hk) {
     const bool is_k = row >= p.Hk;
@@ -804,7 +814,8 @@ int qh_launch_gdn_prep(const QhGdnPrepParams& p, hipStream_t st) {
   } else {
     hipLaunchKernelGGL(gdn_conv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
   }
-  hipLaunchKernelGGL(gdn_norm_gates_kernel, dim3(p.M, 2 * p.Hk + 1), dim3(64), 0, st, p);
+  hipLaunchKernelGGL(gdn_norm_gates_kernel, dim3((unsigned)(((long)p.M * (2 * p.Hk + 1) + 3) / 4)), dim3(256), 0, st,
+                     p);
   return 0;
 }
 
