@@ -345,7 +345,19 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(QhGdnScanParams p,
   const int col = lane & 15, kc = 4 * (lane >> 4);
   float* state = p.state + (size_t)h * DK * DV + cg * 16;
   const float* units = ws + (size_t)h * nch * kUnitFloats;
-  for (int e = tid; e < DK * 16; e += 512) sS[(e & 15) * SST + (e >> 4)] = state[(size_t)(e >> 4) * DV + (e & 15)];
+  {  // the state slice: all four loads of a thread in flight before its LDS stores
+    float sv[DK * 16 / 512];
+#pragma unroll
+    for (int k = 0; k < DK * 16 / 512; ++k) {
+      const int e = tid + 512 * k;
+      sv[k] = state[(size_t)(e >> 4) * DV + (e & 15)];
+    }
+#pragma unroll
+    for (int k = 0; k < DK * 16 / 512; ++k) {
+      const int e = tid + 512 * k;
+      sS[(e & 15) * SST + (e >> 4)] = sv[k];
+    }
+  }
   __syncthreads();
 
   if (w < 4) {
