@@ -23,19 +23,35 @@ constexpr int TP = 32;    // key positions per LDS tile
 constexpr int MAXG = 8;   // query heads per KV head
 
 // ---- q/k norm + RoPE + cache write: one wave per (token, head row) ---------
+// Four (token, head) waves per 256-thread block; the cos / sin values of a
+// lane's dims are loaded with its inputs (clamped to the table row), ahead of
+// the norm, so RoPE waits for no further round trip.
 template <int D>
-__global__ __launch_bounds__(64) void attn_prep_kernel(QhAttnPrepParams p) {
+__global__ __launch_bounds__(256) void attn_prep_kernel(QhAttnPrepParams p) {
   constexpr int NPL = D / 64;
-  const int m = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  const int rows = p.Hq + p.Hkv;
+  const int idx = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (idx >= p.M * rows) return;
+  const int m = idx / rows, row = idx - m * rows;
   const int pos = p.past + m;
   const bool is_q = row < p.Hq;
   const int head = is_q ? row : row - p.Hq;
   const uint16_t* src = is_q ? p.q_all + ((size_t)m * p.Hq + head) * 2 * D
                              : p.k + ((size_t)m * p.Hkv + head) * D;
   const float* nw = is_q ? p.q_norm_w : p.k_norm_w;
-  float v[NPL];
+  float v[NPL], cs[NPL], sn[NPL];
 #pragma unroll
   for (int i = 0; i < NPL; ++i) v[i] = bf2f(src[lane * NPL + i]);
+  if (p.rot > 0) {
+    const float* cr = p.cos_t + (size_t)pos * p.rot;
+    const float* sr = p.sin_t + (size_t)pos * p.rot;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      const int c = min(lane * NPL + i, p.rot - 1);
+      cs[i] = cr[c];
+      sn[i] = sr[c];
+    }
+  }
   if (nw) {
     float ss = 0.0f;
 #pragma unroll
@@ -48,14 +64,12 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(QhAttnPrepParams p) {
   if (p.rot > 0) {
     const int half = p.rot >> 1;
     const int pm = half / NPL;  // partner lane distance (power of two, checked on the host)
-    const float* cr = p.cos_t + (size_t)pos * p.rot;
-    const float* sr = p.sin_t + (size_t)pos * p.rot;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
       const float partner = __shfl_xor(v[i], pm, 64);
       const int c = lane * NPL + i;
-      if (c < half) v[i] = v[i] * cr[c] - partner * sr[c];
-      else if (c < p.rot) v[i] = v[i] * cr[c] + partner * sr[c];
+      if (c < half) v[i] = v[i] * cs[i] - partner * sn[i];
+      else if (c < p.rot) v[i] = v[i] * cs[i] + partner * sn[i];
     }
   }
   if (is_q) {
@@ -760,11 +774,11 @@ int qh_launch_attn_prep(const QhAttnPrepParams& p, hipStream_t st) {
     return -1;
   }
   if (p.M <= 0) return 0;
-  const dim3 grid(p.M, p.Hq + p.Hkv);
+  const dim3 grid((unsigned)(((long)p.M * (p.Hq + p.Hkv) + 3) / 4));
   if (p.D == 256)
-    hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(64), 0, st, p);
+    hipLaunchKernelGGL(attn_prep_kernel<256>, grid, dim3(256), 0, st, p);
   else
-    hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(64), 0, st, p);
+    hipLaunchKernelGGL(attn_prep_kernel<128>, grid, dim3(256), 0, st, p);
   return 0;
 }
 
