@@ -627,9 +627,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const uint16_t* x, GemmGr
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Shape limit of the persistent kernel: its per-tile buffer ranges (64 rows
-// of K bf16) stay below 2^31 bytes.
-inline bool gemm_dma_fits(int K) { return (long)64 * K * 2 < 0x7fffffffL; }
+// Shape limit of the persistent kernel: its per-tile buffer ranges (up to
+// 128 rows of K bf16, 192 rows of K E4M3) stay below 2^31 bytes.
+inline bool gemm_dma_fits(int K) { return (long)128 * K * 2 < 0x7fffffffL; }
 
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* part, int S, int M,
                                                                  int ldp, GemmGroup g, int bn);
