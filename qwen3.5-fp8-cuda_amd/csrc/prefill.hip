@@ -88,17 +88,23 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(QhAttnPrepParams p) {
 }
 
 // ---- causal attention: one workgroup per (KV head, query token) -------------
-// The 4 waves serve the query heads of the GQA group (heads wid, wid + 4);
-// K/V tiles of 32 positions are staged in LDS and shared by those heads.
-template <int D>
+// The 4 waves serve the query heads of the GQA group (heads wid, wid + 4, ...:
+// HPW = ceil(G / 4) per wave); K/V tiles of 32 positions are staged in LDS and
+// shared by those heads.  The tile loads are branch-free (rows past the
+// query's last key read row t0 and are zeroed when staged) and the next tile
+// is requested before the current one is used; the per-position dot product
+// and the P V sum have constant trip counts and are unrolled, so their LDS
+// reads go out together.  The arithmetic order is fixed: lane half h sums the
+// q k products of dims h D/2 .. h D/2 + D/2 - 1 in order, the halves are
+// added, and P V adds positions in order.
+template <int D, int HPW>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(QhAttnPrefillParams p) {
   constexpr int NPL = D / 64;
   constexpr int KS = D + 8;
-  constexpr int HPW = MAXG / 4;
-  __shared__ float sQ[MAXG][D];
+  __shared__ __align__(16) float sQ[4 * HPW][D];
   __shared__ __align__(16) uint16_t sK[TP * KS];
   __shared__ __align__(16) uint16_t sV[TP * D];
-  __shared__ float sP[MAXG][TP];
+  __shared__ __align__(16) float sP[4 * HPW][TP];
   const int kvh = blockIdx.x, m = blockIdx.y;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int G = p.Hq / p.Hkv;
@@ -106,15 +112,55 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(QhAttnPrefillParams p
   const uint16_t* kbase = p.k_cache + (size_t)kvh * p.max_seq * D;
   const uint16_t* vbase = p.v_cache + (size_t)kvh * p.max_seq * D;
 
-  float gate_v[HPW][NPL];
-  for (int gi = wid; gi < G; gi += 4) {
+  // K/V tile staging: each thread moves PER 16-byte pieces of K and of V
+  constexpr int PER = TP * (D / 8) / 256;
+  u32x4 kreg[PER], vreg[PER];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int idx = threadIdx.x + 256 * e;
+      const int pos = t0 + idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const int src = pos < total ? pos : t0;
+      kreg[e] = *(const u32x4*)(kbase + (size_t)src * D + c8);
+      vreg[e] = *(const u32x4*)(vbase + (size_t)src * D + c8);
+    }
+  };
+  auto stage = [&](int t0) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int idx = threadIdx.x + 256 * e;
+      const int row = idx / (D / 8);
+      const int c8 = (idx % (D / 8)) * 8;
+      const bool in = t0 + row < total;
+      *(u32x4*)(sK + row * KS + c8) = in ? kreg[e] : zero;
+      *(u32x4*)(sV + row * D + c8) = in ? vreg[e] : zero;
+    }
+  };
+  // the query heads and gates first (unconditional loads: a slot past the
+  // group reads head 0 and is not used), then the first tile
+  float qv[HPW][NPL], gate_v[HPW][NPL];
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi < G ? wid + 4 * hi : 0;
     const int h = kvh * G + gi;
     const float* q = p.q + ((size_t)m * p.Hq + h) * D;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) sQ[gi][lane * NPL + i] = q[lane * NPL + i];
     const uint16_t* gp = p.gate + (size_t)m * p.gate_mstride + (size_t)h * p.gate_hstride;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) gate_v[gi >> 2][i] = bf2f(gp[lane * NPL + i]);
+    for (int i = 0; i < NPL; ++i) {
+      qv[hi][i] = q[lane * NPL + i];
+      gate_v[hi][i] = bf2f(gp[lane * NPL + i]);
+    }
+  }
+  fetch(0);
+#pragma unroll
+  for (int hi = 0; hi < HPW; ++hi) {
+    const int gi = wid + 4 * hi;
+    if (gi < G) {
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) sQ[gi][lane * NPL + i] = qv[hi][i];
+    }
   }
   float mx[HPW], l[HPW], o[HPW][NPL];
 #pragma unroll
@@ -125,41 +171,40 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(QhAttnPrefillParams p
     for (int i = 0; i < NPL; ++i) o[hi][i] = 0.0f;
   }
   const float scale = rsqrtf((float)D);
+  const int prow = lane >> 1, half = lane & 1;
   for (int t0 = 0; t0 < total; t0 += TP) {
+    stage(t0);
     __syncthreads();
-    for (int e = threadIdx.x; e < TP * (D / 8); e += 256) {
-      const int row = e / (D / 8), c8 = (e % (D / 8)) * 8;
-      const int pos = t0 + row;
-      u32x4 kq = {0u, 0u, 0u, 0u}, vq = {0u, 0u, 0u, 0u};
-      if (pos < total) {
-        kq = *(const u32x4*)(kbase + (size_t)pos * D + c8);
-        vq = *(const u32x4*)(vbase + (size_t)pos * D + c8);
-      }
-      *(u32x4*)(sK + row * KS + c8) = kq;
-      *(u32x4*)(sV + row * D + c8) = vq;
-    }
-    __syncthreads();
-    const int prow = lane >> 1, half = lane & 1;
+    if (t0 + TP < total) fetch(t0 + TP);
     const bool valid = t0 + prow < total;
 #pragma unroll
     for (int hi = 0; hi < HPW; ++hi) {
       const int gi = wid + 4 * hi;
       if (gi < G) {
-        float dot = 0.0f;
-        for (int c = half * (D / 2); c < (half + 1) * (D / 2); c += 8) {
-          const u32x4 k8 = *(const u32x4*)(sK + prow * KS + c);
-          const uint32_t kw[4] = {k8.x, k8.y, k8.z, k8.w};
+        const uint16_t* kr = sK + prow * KS + half * (D / 2);
+        const float* qr = &sQ[gi][half * (D / 2)];
+        u32x4 k8[D / 16];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            dot = fmaf(sQ[gi][c + 2 * u], bf_lo(kw[u]), dot);
-            dot = fmaf(sQ[gi][c + 2 * u + 1], bf_hi(kw[u]), dot);
-          }
+        for (int cc = 0; cc < D / 16; ++cc) k8[cc] = *(const u32x4*)(kr + 8 * cc);
+        float dot = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < D / 16; ++cc) {
+          const float4 qa = *(const float4*)(qr + 8 * cc);
+          const float4 qb = *(const float4*)(qr + 8 * cc + 4);
+          dot = fmaf(qa.x, bf_lo(k8[cc].x), dot);
+          dot = fmaf(qa.y, bf_hi(k8[cc].x), dot);
+          dot = fmaf(qa.z, bf_lo(k8[cc].y), dot);
+          dot = fmaf(qa.w, bf_hi(k8[cc].y), dot);
+          dot = fmaf(qb.x, bf_lo(k8[cc].z), dot);
+          dot = fmaf(qb.y, bf_hi(k8[cc].z), dot);
+          dot = fmaf(qb.z, bf_lo(k8[cc].w), dot);
+          dot = fmaf(qb.w, bf_hi(k8[cc].w), dot);
         }
         dot += __shfl_xor(dot, 1, 64);
-        const float s = valid ? dot * scale : -INFINITY;
-        const float nm = fmaxf(mx[hi], wave_max(s));
+        const float sc = valid ? dot * scale : -INFINITY;
+        const float nm = fmaxf(mx[hi], wave_max(sc));
         const float corr = __expf(mx[hi] - nm);
-        const float pv = valid ? __expf(s - nm) : 0.0f;
+        const float pv = valid ? __expf(sc - nm) : 0.0f;
         l[hi] = l[hi] * corr + wave_sum(half == 0 ? pv : 0.0f);
         mx[hi] = nm;
         if (half == 0) sP[gi][prow] = pv;
@@ -172,13 +217,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(QhAttnPrefillParams p
     for (int hi = 0; hi < HPW; ++hi) {
       const int gi = wid + 4 * hi;
       if (gi < G) {
-        for (int j = 0; j < TP; ++j) {
-          const float pj = sP[gi][j];
 #pragma unroll
-          for (int i = 0; i < NPL; ++i) o[hi][i] = fmaf(pj, bf2f(sV[j * D + lane * NPL + i]), o[hi][i]);
+        for (int j4 = 0; j4 < TP / 4; ++j4) {
+          const float4 p4 = *(const float4*)&sP[gi][4 * j4];
+          const float pj[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint16_t* vr = sV + (4 * j4 + u) * D + lane * NPL;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) o[hi][i] = fmaf(pj[u], bf2f(vr[i]), o[hi][i]);
+          }
         }
       }
     }
+    __syncthreads();
   }
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
@@ -802,10 +854,11 @@ int qh_launch_attn_prefill(const QhAttnPrefillParams& p, hipStream_t st) {
     return 0;
   }
   const dim3 grid(p.Hkv, p.M);
-  if (p.D == 256)
-    hipLaunchKernelGGL(attn_prefill_kernel<256>, grid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, st, p);
+  const bool g4 = p.Hq <= 4 * p.Hkv;  // one query head per wave
+  void (*fn)(QhAttnPrefillParams) =
+      p.D == 256 ? (g4 ? attn_prefill_kernel<256, 1> : attn_prefill_kernel<256, 2>)
+                 : (g4 ? attn_prefill_kernel<128, 1> : attn_prefill_kernel<128, 2>);
+  hipLaunchKernelGGL(fn, grid, dim3(256), 0, st, p);
   return 0;
 }
 

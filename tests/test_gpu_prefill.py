@@ -26,10 +26,14 @@ def cu(t):
 # positions past .. tokens-1 are the prefill.  Prefills of 256 or more tokens
 # run the matrix-core kernel (300: a ragged last 32-token block; 330 - 70 =
 # 260 after a cached prefix), shorter ones the per-token kernel.
-@pytest.mark.parametrize("M,past", [(37, 0), (70, 0), (100, 20), (256, 0), (300, 0), (330, 70)])
-def test_attention_prefill(M, past):
+# The last two cases take the per-token kernel with two query heads per wave
+# (8 per KV head, head dim 128) and with an idle wave (3 per KV head).
+@pytest.mark.parametrize("M,past,Hq,Hkv,D", [(37, 0, 8, 2, 256), (70, 0, 8, 2, 256), (100, 20, 8, 2, 256),
+                                             (256, 0, 8, 2, 256), (300, 0, 8, 2, 256), (330, 70, 8, 2, 256),
+                                             (45, 10, 16, 2, 128), (50, 13, 6, 2, 256)])
+def test_attention_prefill(M, past, Hq, Hkv, D):
     g = gen(21)
-    Hq, Hkv, D, rot, max_seq = 8, 2, 256, 64, 512
+    rot, max_seq = 64, 512
     q_all = bf(randn(g, M, Hq, 2 * D))
     k, v = bf(randn(g, M, Hkv, D)), bf(randn(g, M, Hkv, D))
     qn_w, kn_w = randn(g, D, std=0.1), randn(g, D, std=0.1)
