@@ -752,28 +752,42 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* pa
   const int S = SC > 0 ? SC : S_arg;
   const int m = blockIdx.x, t = threadIdx.x, nv = N >> 3;
   uint16_t* hr = h + (size_t)m * N;
+  // Every load first, at a clamped vector index (a vector past nv is loaded
+  // and not used), so the partial slices, the residual row and the norm
+  // weights share one round trip; the weights through a buffer resource
+  // (none when w is null: an empty range, the loads read 0).
+  const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(w), (short)0, w ? N * 4 : 0, 0x00020000);
+  f32x4 a0[V], a1[V];
+  u32x4 hv[V], wq[V][2];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int ic = min(t + 256 * v, nv - 1);
+    const float* p0 = part + (size_t)m * ldp + 8 * ic;
+    a0[v] = *(const f32x4*)p0;
+    a1[v] = *(const f32x4*)(p0 + 4);
+#pragma unroll
+    for (int z = 1; z < S; ++z) {
+      const float* pz = p0 + (size_t)z * M * ldp;
+      a0[v] += *(const f32x4*)pz;
+      a1[v] += *(const f32x4*)(pz + 4);
+    }
+    hv[v] = *(const u32x4*)(hr + 8 * ic);
+    wq[v][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)ic * 32u, 0, 0);
+    wq[v][1] = __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)ic * 32u + 16u, 0, 0);
+  }
   float xv[V][8];
   float ss = 0.0f;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int i = t + 256 * v;
     if (i < nv) {
-      const float* p0 = part + (size_t)m * ldp + 8 * i;
-      f32x4 a0 = *(const f32x4*)p0, a1 = *(const f32x4*)(p0 + 4);
-#pragma unroll
-      for (int z = 1; z < S; ++z) {
-        const float* pz = p0 + (size_t)z * M * ldp;
-        a0 += *(const f32x4*)pz;
-        a1 += *(const f32x4*)(pz + 4);
-      }
-      const u32x4 hv = *(const u32x4*)(hr + 8 * i);
       u32x4 sum;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float o_lo = rbf(q < 2 ? a0[2 * q] : a1[2 * q - 4]);
-        const float o_hi = rbf(q < 2 ? a0[2 * q + 1] : a1[2 * q - 3]);
-        xv[v][2 * q] = rbf(bf_lo(hv[q]) + o_lo);
-        xv[v][2 * q + 1] = rbf(bf_hi(hv[q]) + o_hi);
+        const float o_lo = rbf(q < 2 ? a0[v][2 * q] : a1[v][2 * q - 4]);
+        const float o_hi = rbf(q < 2 ? a0[v][2 * q + 1] : a1[v][2 * q - 3]);
+        xv[v][2 * q] = rbf(bf_lo(hv[v][q]) + o_lo);
+        xv[v][2 * q + 1] = rbf(bf_hi(hv[v][q]) + o_hi);
         sum[q] = (__float_as_uint(xv[v][2 * q]) >> 16) | (__float_as_uint(xv[v][2 * q + 1]) & 0xFFFF0000u);
       }
       *(u32x4*)(hr + 8 * i) = sum;
@@ -789,8 +803,9 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(const float* pa
   for (int v = 0; v < V; ++v) {
     const int i = t + 256 * v;
     if (i < nv) {
-      const float4 w0 = *(const float4*)(w + 8 * i), w1 = *(const float4*)(w + 8 * i + 4);
-      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      float wv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wv[e] = __uint_as_float(wq[v][e >> 2][e & 3]);
       u32x4 y;
 #pragma unroll
       for (int q = 0; q < 4; ++q)

@@ -83,15 +83,30 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(uint16_t* h, cons
   const int t = threadIdx.x, nv = D >> 3;
   uint16_t* hr = h + (size_t)blockIdx.x * D;
   const uint16_t* orow = o ? o + (size_t)blockIdx.x * D : nullptr;
+  // Every load first, at a clamped vector index (a vector past nv is loaded
+  // and not used), so h, o and the norm weights share one round trip; o
+  // through a buffer resource (an empty range when o is null).
+  const auto orr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(orow), (short)0, orow ? D * 2 : 0,
+                                                     0x00020000);
+  u32x4 av[V], bv[V];
+  float4 wv0[V], wv1[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int ic = min(t + 256 * v, nv - 1);
+    av[v] = *(const u32x4*)(hr + 8 * ic);
+    bv[v] = __builtin_amdgcn_raw_buffer_load_b128(orr, (uint32_t)ic * 16u, 0, 0);
+    wv0[v] = *(const float4*)(w + 8 * ic);
+    wv1[v] = *(const float4*)(w + 8 * ic + 4);
+  }
   float xv[V][8];
   float ss = 0.0f;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int i = t + 256 * v;
     if (i < nv) {
-      u32x4 a = *(const u32x4*)(hr + 8 * i);
+      u32x4 a = av[v];
       if (orow) {
-        const u32x4 b = *(const u32x4*)(orow + 8 * i);
+        const u32x4 b = bv[v];
         u32x4 sum;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -117,7 +132,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_rows_kernel(uint16_t* h, cons
   for (int v = 0; v < V; ++v) {
     const int i = t + 256 * v;
     if (i < nv) {
-      const float4 w0 = *(const float4*)(w + 8 * i), w1 = *(const float4*)(w + 8 * i + 4);
+      const float4 w0 = wv0[v], w1 = wv1[v];
       const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
       u32x4 y;
 #pragma unroll
@@ -149,7 +164,7 @@ __global__ void embed_gather_kernel(const uint16_t* table, const int64_t* ids, u
 namespace {
 bool rows_vectorizable(const void* a, const void* b, const void* w, const void* out, int D) {
   const auto al = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
-  return D % 8 == 0 && D <= 2048 * 4 && al(a) && al(b) && al(w) && al(out);
+  return D > 0 && D % 8 == 0 && D <= 2048 * 4 && al(a) && al(b) && al(w) && al(out);
 }
 
 template <int V>
@@ -173,7 +188,7 @@ bool launch_add_rmsnorm_vec(void* h, const void* o, const float* w, void* out, i
 
 void qh_launch_rmsnorm_rows(const void* x, const float* w, void* out, int rows, int D, float eps,
                             hipStream_t st) {
-  if (rows <= 0) return;
+  if (rows <= 0 || D <= 0) return;
   if (launch_add_rmsnorm_vec(const_cast<void*>(x), nullptr, w, out, rows, D, eps, st)) return;
   hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, (const uint16_t*)x, w,
                      (uint16_t*)out, D, eps);
@@ -181,7 +196,7 @@ void qh_launch_rmsnorm_rows(const void* x, const float* w, void* out, int rows, 
 
 void qh_launch_add_rmsnorm_rows(void* h, const void* o, const float* w, void* out, int rows, int D,
                                 float eps, hipStream_t st) {
-  if (rows <= 0) return;
+  if (rows <= 0 || D <= 0) return;
   if (launch_add_rmsnorm_vec(h, o, w, out, rows, D, eps, st)) return;
   qh_launch_add_bf16(h, o, h, rows * D, st);
   hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, st, (const uint16_t*)h, w,
