@@ -110,6 +110,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(QhGdnScanParams p, 
   // them token-major (K) and, transposed in registers (v_perm), as 16-byte
   // rows of the dim-major tile (2-byte scatter stores hit 8-way LDS bank
   // conflicts); every thread also copies 4 16-byte pieces of Q.
+  // the chunk's log decay and write strength per token, requested with the
+  // tiles below (every thread loads; threads tid < CH keep them)
+  const bool tok_ok = t0 + lane < p.M;
+  const int tok = tok_ok ? t0 + lane : p.M - 1;
+  const float g_tok = p.g[(size_t)tok * p.Hv + h];
+  const float b_tok = bf2f(p.beta[(size_t)tok * p.Hv + h]);
   {
     const u32x4 zero = {0u, 0u, 0u, 0u};
     const bool is_v = tid >= 128;  // wave-uniform
@@ -148,12 +154,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(QhGdnScanParams p, 
     }
   }
   if (tid < CH) {
-    const bool ok = t0 + tid < p.M;
-    const int t = ok ? t0 + tid : p.M - 1;
-    const float gv = p.g[(size_t)t * p.Hv + h];
-    const float bv = bf2f(p.beta[(size_t)t * p.Hv + h]);
-    sG[tid] = ok ? gv : 0.0f;  // padding: no decay, no write
-    sB[tid] = ok ? bv : 0.0f;
+    sG[tid] = tok_ok ? g_tok : 0.0f;  // padding: no decay, no write
+    sB[tid] = tok_ok ? b_tok : 0.0f;
   }
   __syncthreads();
   if (w == 0) {  // inclusive cumulative sum of the log decays
