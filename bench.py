@@ -169,7 +169,7 @@ def prefill_gemm_launchers(inputs):
         y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
         def run(x=x, w=w, s=s, y=y, M=M, N=N, K=K):
             abi.check(lib.qh_gemm_e4m3(abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M, N, K,
-                                       K // 128, 0, None, abi.stream_handle()), "gemm")
+                                       K // 128, 0, None, 0, abi.stream_handle()), "gemm")
         out.append(((M, N, K), run))
     return out
 

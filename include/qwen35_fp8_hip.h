@@ -197,8 +197,10 @@ int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_strid
  * cannot allocate (code under HIP graph capture, serving loops that forbid
  * hipMalloc): the split partials and arrival counters live in a fixed
  * library array (4 MiB + 256 bytes per GPU, held until the process ends).
- * Limits: n_kv <= 64, nsplit 1..64, n_kv * nsplit * 4 * (head_dim + 2) <= 2^20
- * floats; larger shapes return -1.  The first call on a device looks up the
+ * Limits: n_kv <= 64, nsplit 1..64, n_heads / n_kv <= 8 and
+ * n_kv * nsplit * 8 * (head_dim + 2) <= 2^20 partial floats, i.e.
+ * qh_attn_scratch_bytes(n_kv, nsplit, head_dim) <= 4 MiB (partials are laid
+ * out for up to 8 query heads per KV head); larger shapes return -1.  The first call on a device looks up the
  * array's address (make it outside graph capture).  Every call on one GPU
  * shares the array: calls that overlap on one GPU race. */
 int qh_attn_decode_noalloc(const void* q, int q_stride, const void* gate, int gate_stride,
@@ -289,14 +291,17 @@ int qh_gemv_e4m3_gated(const void* core, const void* z, const void* norm_w, int 
                        const void* res, const void* w, const void* s, void* y, int n, int kb,
                        int scales_bf16, qh_stream_t stream);
 
-/* Workspace bytes for qh_gemm_e4m3 / qh_gemm_e4m3_grouped (a fixed 16 MiB of
- * split-K partials, whatever M and K).  The workspace is optional: without one
- * the GEMM does not split K.  Calls sharing a workspace must not overlap. */
+/* Workspace bytes for qh_gemm_e4m3 / qh_gemm_e4m3_grouped /
+ * qh_gemm_e4m3_add_rmsnorm (a fixed 16 MiB of split-K partials, whatever M and
+ * K).  The workspace is optional: with ws null the GEMM does not split K.  A
+ * non-null ws must come with ws_bytes >= this size and be 256-byte aligned, or
+ * the call fails before any launch; no plan puts more partials in it than
+ * ws_bytes.  Calls sharing a workspace must not overlap. */
 size_t qh_gemm_workspace_size(int M, int K);
 
 /* Prefill GEMM on the fp8 matrix cores (fp8_gemm_batch semantics). */
 int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
-                 int kb, int scales_bf16, void* ws, qh_stream_t stream);
+                 int kb, int scales_bf16, void* ws, size_t ws_bytes, qh_stream_t stream);
 
 /* Output projection + residual add + (1+w) RMSNorm, the batch prefill's step
  * after o_proj / out_proj / down: o = bf16(x . deq(W)^T) (M x N scratch, not
@@ -307,7 +312,7 @@ int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, in
  * the norm as separate steps. */
 int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
                              int kb, int scales_bf16, void* h, const float* norm_w, void* hn, float eps,
-                             void* ws, qh_stream_t stream);
+                             void* ws, size_t ws_bytes, qh_stream_t stream);
 
 /* Grouped prefill GEMM; no counterpart in the reference, which runs each
  * projection as its own fp8_gemm_batch (main.py:262-269).  Up to 4 projections
@@ -317,7 +322,7 @@ int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0, 
                          void* y0, int n0, int kb0, const void* w1, const void* s1, void* y1,
                          int n1, int kb1, const void* w2, const void* s2, void* y2, int n2,
                          int kb2, const void* w3, const void* s3, void* y3, int n3, int kb3,
-                         int scales_bf16, void* ws, qh_stream_t stream);
+                         int scales_bf16, void* ws, size_t ws_bytes, qh_stream_t stream);
 
 /* ---- batch prefill pieces (the reference runs these in torch) ---------- */
 

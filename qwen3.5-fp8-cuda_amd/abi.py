@@ -84,9 +84,9 @@ NATIVE_SIGNATURES = {
     "qh_linear_gates": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]),
     "qh_gated_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i, _vp]),
     "qh_gemm_workspace_size": (_sz, [_i, _i]),
-    "qh_gemm_e4m3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]),
-    "qh_gemm_e4m3_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _f, _vp, _vp]),
-    "qh_gemm_e4m3_grouped": (_i, [_vp, _i, _i, _i] + [_vp, _vp, _vp, _i, _i] * 4 + [_i, _vp, _vp]),
+    "qh_gemm_e4m3": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "qh_gemm_e4m3_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _f, _vp, _sz, _vp]),
+    "qh_gemm_e4m3_grouped": (_i, [_vp, _i, _i, _i] + [_vp, _vp, _vp, _i, _i] * 4 + [_i, _vp, _sz, _vp]),
     "qh_attn_prep": (_i, [_vp] * 10 + [_i] * 7 + [_f, _vp]),
     "qh_attn_prefill": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp] + [_i] * 6 + [_vp]),
     "qh_gdn_prep": (_i, [_vp] * 12 + [_i] * 6 + [_vp]),

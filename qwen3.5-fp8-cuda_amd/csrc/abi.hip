@@ -739,14 +739,34 @@ QH_EXPORT int qh_gated_rmsnorm(const void* core, const void* z, const void* w, v
 
 QH_EXPORT size_t qh_gemm_workspace_size(int M, int K) { return qh_gemm_workspace_bytes(M, K); }
 
+// A caller workspace for split-K partials is either absent (ws null: K is not
+// split) or ws_bytes >= qh_gemm_workspace_size bytes, 256-byte aligned.  The
+// check runs before anything touches the device, and the plan never puts more
+// partials in the workspace than ws_bytes.
+static bool gemm_ws_ok(const void* ws, size_t ws_bytes, int M, int K, const char* what) {
+  if (!ws) return true;
+  const size_t need = qh_gemm_workspace_bytes(M, K);
+  if (ws_bytes < need) {
+    qh_set_error("%s: workspace of %zu bytes is smaller than qh_gemm_workspace_size (%zu)", what, ws_bytes,
+                 need);
+    return false;
+  }
+  if ((uintptr_t)ws % 256 != 0) {
+    qh_set_error("%s: workspace must be 256-byte aligned", what);
+    return false;
+  }
+  return true;
+}
+
 // Prefill block-scaled E4M3 GEMM: Y[M,N] = bf16(X[M,K] . deq(W)[N,K]^T) on the
-// fp8 matrix cores.  `ws` (qh_gemm_workspace_size bytes, optional) holds
+// fp8 matrix cores.  `ws` (ws_bytes >= qh_gemm_workspace_size, optional) holds
 // split-K partials; without it the GEMM does not split K.
 QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N,
-                           int K, int kb, int scales_bf16, void* ws, hipStream_t stream) {
+                           int K, int kb, int scales_bf16, void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!k_ok(K, "qh_gemm_e4m3")) return -1;
+  if (!gemm_ws_ok(ws, ws_bytes, M, K, "qh_gemm_e4m3")) return -1;
   if (M <= 0 || N <= 0) return 0;
-  const int rc = ws ? qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scales_bf16 != 0, ws, stream)
+  const int rc = ws ? qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scales_bf16 != 0, ws, ws_bytes, stream)
                     : qh_launch_gemm_e4m3(x, w, s, y, M, N, K, kb, scales_bf16 != 0, stream);
   if (rc != 0) return -1;
   return check_launch("qh_gemm_e4m3");
@@ -759,11 +779,12 @@ QH_EXPORT int qh_gemm_e4m3(const void* x, const void* w, const void* s, void* y,
 // (1 + norm_w) (norm_w null: the add only).
 QH_EXPORT int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
                                        int kb, int scales_bf16, void* h, const float* norm_w, void* hn, float eps,
-                                       void* ws, hipStream_t stream) {
+                                       void* ws, size_t ws_bytes, hipStream_t stream) {
   if (K <= 0 || K % 128 != 0) {
     qh_set_error("qh_gemm_e4m3_add_rmsnorm: K=%d must be a positive multiple of 128", K);
     return -1;
   }
+  if (!gemm_ws_ok(ws, ws_bytes, M, K, "qh_gemm_e4m3_add_rmsnorm")) return -1;
   if (M < 0 || N < 0) {
     qh_set_error("qh_gemm_e4m3_add_rmsnorm: bad shape M=%d N=%d", M, N);
     return -1;
@@ -778,7 +799,7 @@ QH_EXPORT int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void*
     return -1;
   }
   if (qh_launch_gemm_e4m3_add_rmsnorm(x, w, s, o, M, N, K, kb, scales_bf16 != 0, h, norm_w, hn, eps, ws,
-                                      stream) != 0)
+                                      ws_bytes, stream) != 0)
     return -1;
   return check_launch("qh_gemm_e4m3_add_rmsnorm");
 }
@@ -787,14 +808,15 @@ QH_EXPORT int qh_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void*
 // projection as its own fp8_gemm_batch, main.py:262-269).  Up to 4
 // projections of the same activation X[M, K] -- segment t:
 // Y_t[M, n_t] = bf16(X . deq(W_t)^T), scale mode kb_t -- with one activation
-// split and one launch.  `ws` as for qh_gemm_e4m3 (optional).
+// split and one launch.  `ws` / `ws_bytes` as for qh_gemm_e4m3 (optional).
 QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const void* w0,
                                    const void* s0, void* y0, int n0, int kb0, const void* w1,
                                    const void* s1, void* y1, int n1, int kb1, const void* w2,
                                    const void* s2, void* y2, int n2, int kb2, const void* w3,
                                    const void* s3, void* y3, int n3, int kb3, int scales_bf16,
-                                   void* ws, hipStream_t stream) {
+                                   void* ws, size_t ws_bytes, hipStream_t stream) {
   if (!k_ok(K, "qh_gemm_e4m3_grouped")) return -1;
+  if (!gemm_ws_ok(ws, ws_bytes, M, K, "qh_gemm_e4m3_grouped")) return -1;
   if (!x) {
     qh_set_error("qh_gemm_e4m3_grouped: null activation");
     return -1;
@@ -802,7 +824,7 @@ QH_EXPORT int qh_gemm_e4m3_grouped(const void* x, int M, int K, int nseg, const 
   if (M <= 0) return 0;
   const QhGemmSeg seg[4] = {{w0, s0, y0, n0, kb0}, {w1, s1, y1, n1, kb1},
                             {w2, s2, y2, n2, kb2}, {w3, s3, y3, n3, kb3}};
-  if (qh_launch_gemm_e4m3_group_ws(x, M, K, seg, nseg, scales_bf16 != 0, ws, stream) != 0) return -1;
+  if (qh_launch_gemm_e4m3_group_ws(x, M, K, seg, nseg, scales_bf16 != 0, ws, ws_bytes, stream) != 0) return -1;
   return check_launch("qh_gemm_e4m3_grouped");
 }
 

@@ -537,7 +537,7 @@ size_t qh_attn_scratch_floats(int n_kv, int nsplit, int head_dim) {
 }
 
 int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
-  if (p.n_kv <= 0 || p.n_heads % p.n_kv != 0 || p.n_heads / p.n_kv > MAXG) {
+  if (p.n_kv <= 0 || p.n_heads <= 0 || p.n_heads % p.n_kv != 0 || p.n_heads / p.n_kv > MAXG) {
     qh_set_error("attn: n_heads=%d n_kv_heads=%d unsupported (group size must divide and be <= %d)",
                  p.n_heads, p.n_kv, MAXG);
     return -1;
@@ -579,7 +579,8 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
 // counters live in the file-scope array above instead of caller memory.  No
 // counterpart in the reference; for callers that cannot allocate (code under
 // graph capture, serving loops that forbid hipMalloc).  Limits: n_kv <= 64
-// and n_kv * nsplit * 4 * (head_dim + 2) <= 2^20 partial floats (4 MiB).
+// and qh_attn_scratch_floats = n_kv * nsplit * MAXG * (head_dim + 2) <= 2^20
+// partial floats (4 MiB).
 // Calls that overlap on one GPU race on the shared array.
 extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
     const void* q, int q_stride, const void* gate, int gate_stride, const void* k_new,
@@ -591,8 +592,8 @@ extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
       (head_dim != 128 && head_dim != 256) ||
       qh_attn_scratch_floats(n_kv, nsplit, head_dim) > kStaticPartFloats) {
     qh_set_error("qh_attn_decode_noalloc: n_kv=%d, nsplit=%d, head_dim=%d exceed the fixed "
-                 "scratch (n_kv <= %d, nsplit 1..64, n_kv*nsplit*4*(head_dim+2) <= %zu floats)",
-                 n_kv, nsplit, head_dim, kStaticCounterWords, kStaticPartFloats);
+                 "scratch (n_kv <= %d, nsplit 1..64, n_kv*nsplit*%d*(head_dim+2) <= %zu floats)",
+                 n_kv, nsplit, head_dim, kStaticCounterWords, MAXG, kStaticPartFloats);
     return -1;
   }
   uint32_t* ws = static_scratch(stream);

@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) void delta_rule_kernel(const uint16_t* q, cons
 }  // namespace
 
 int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st) {
-  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0) {
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv <= 0 || p.Hv % p.Hk != 0) {
     qh_set_error("gdn: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk = dv = 128)", p.dk, p.dv,
                  p.Hk, p.Hv);
     return -1;
@@ -370,7 +370,7 @@ int qh_launch_gdn_decode(const QhGdnParams& p, hipStream_t st) {
 }
 
 int qh_launch_gdn_decode_core(const QhGdnParams& p, hipStream_t st) {
-  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0 || p.Hv % 8 != 0) {
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv <= 0 || p.Hv % p.Hk != 0 || p.Hv % 8 != 0) {
     qh_set_error("gdn_core: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d; need dk = dv = 128, Hv %% 8 == 0)",
                  p.dk, p.dv, p.Hk, p.Hv);
     return -1;

@@ -513,7 +513,7 @@ size_t qh_gdn_chunk_ws_bytes(int M, int Hv) {
 }
 
 int qh_launch_gdn_chunk(const QhGdnScanParams& p, float* ws, size_t ws_bytes, hipStream_t st) {
-  if (p.dk != DK || p.dv != DV || p.Hk <= 0 || p.Hv % p.Hk != 0) {
+  if (p.dk != DK || p.dv != DV || p.Hk <= 0 || p.Hv <= 0 || p.Hv % p.Hk != 0) {
     qh_set_error("gdn_chunk: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d)", p.dk, p.dv, p.Hk, p.Hv);
     return -1;
   }

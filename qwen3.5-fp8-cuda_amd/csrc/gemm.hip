@@ -900,7 +900,7 @@ constexpr GemmShape kGemmShapes[] = {{64, 64, 3, 2030.0, 2460.0}, {64, 128, 2, 2
 // 2560 took 17.7 us unsplit and 21.9 us in two slices).  Deeper rings for
 // 64 x 64 tiles (three or four stages, fewer workgroups per CU) measured no
 // faster at M = 128 and 512.
-GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const void* ws) {
+GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const void* ws, size_t ws_bytes) {
   const int KB = K / 128;
   GemmPlan best = {64, 64, 3, 1};
   double best_t = 1e300;
@@ -911,7 +911,7 @@ GemmPlan gemm_plan(int M, int K, const QhGemmSeg* seg, int nseg, int cus, const 
     const long slots = (long)cus * c.wpc / 8;  // workgroups per XCD
     for (int S = 1; S <= 8; ++S) {
       if (S > 1 && (!ws || KB % S != 0 || KB / S < 4 ||
-                    (size_t)S * M * tiles_n * c.bn * sizeof(float) > kSplitPartBytes))
+                    (size_t)S * M * tiles_n * c.bn * sizeof(float) > ws_bytes))
         continue;
       const long items = tiles_m * ((tiles_n + 7) / 8) * S;
       const long per_wg = (items + slots - 1) / slots;
@@ -940,11 +940,11 @@ void launch_gemm_plan(const GemmPlan& pl, const uint16_t* x, const QhGemmSeg* se
 // Split-K for the per-workgroup fallback kernel (caller workspace only) when
 // there are no more tiles than CUs: the largest S <= 8 dividing the K blocks
 // with >= 4 blocks per slice and S * tiles <= 3 per CU.
-int gemm_split_count(int K, long tiles, int cus, const void* ws) {
+int gemm_split_count(int K, long tiles, int cus, const void* ws, size_t ws_bytes) {
   const int KB = K / 128;
   for (int c = 8; ws && c >= 2 && tiles <= cus; --c)
     if (KB % c == 0 && KB / c >= 4 && tiles * c <= 3L * cus &&
-        (size_t)tiles * c * 64 * 64 * sizeof(float) <= kSplitPartBytes)
+        (size_t)tiles * c * 64 * 64 * sizeof(float) <= ws_bytes)
       return c;
   return 1;
 }
@@ -957,7 +957,7 @@ size_t qh_gemm_workspace_bytes(int M, int K) {
 }
 
 int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* seg, int nseg,
-                                 bool scale_bf16, void* ws, hipStream_t st) {
+                                 bool scale_bf16, void* ws, size_t ws_bytes, hipStream_t st) {
   if (K <= 0 || K % 128 != 0 || M <= 0) {
     qh_set_error("gemm: M=%d, K=%d: need M > 0 and K a positive multiple of 128", M, K);
     return -1;
@@ -997,12 +997,12 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
   for (int t = 0; t < nseg; ++t)
     ring = ring && (uintptr_t)seg[t].w % 16 == 0 && (uintptr_t)seg[t].s % 4 == 0;
   if (ring) {
-    const GemmPlan pl = gemm_plan(M, K, seg, nseg, cus, ws);
+    const GemmPlan pl = gemm_plan(M, K, seg, nseg, cus, ws, ws_bytes);
     if (scale_bf16) launch_gemm_plan<uint16_t>(pl, xa, seg, nseg, M, K, st, cus, part, true);
     else launch_gemm_plan<float>(pl, xa, seg, nseg, M, K, st, cus, part, true);
     return 0;
   }
-  const int S = gemm_split_count(K, tiles, cus, ws);
+  const int S = gemm_split_count(K, tiles, cus, ws, ws_bytes);
   if (scale_bf16) launch_gemm_small<uint16_t>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   else launch_gemm_small<float>(xa, seg, nseg, M, K, tiles, st, cus, S, part);
   return 0;
@@ -1016,7 +1016,7 @@ int qh_launch_gemm_e4m3_group_ws(const void* x, int M, int K, const QhGemmSeg* s
 // add + norm kernel follows.
 int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s, void* o, int M, int N, int K,
                                     int kb, bool scale_bf16, void* h, const float* norm_w, void* hn, float eps,
-                                    void* ws, hipStream_t st) {
+                                    void* ws, size_t ws_bytes, hipStream_t st) {
   const auto al16 = [](const void* p) { return p == nullptr || (uintptr_t)p % 16 == 0; };
   if (M > 0 && N > 0 && K > 0 && K % 128 == 0 && ws && x && (uintptr_t)x % 16 == 0 && w && s &&
       (uintptr_t)w % 16 == 0 && (uintptr_t)s % 4 == 0 && gemm_dma_fits(K) && N % 8 == 0 && N <= 8192 &&
@@ -1026,7 +1026,7 @@ int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s,
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       cus = 256;
     const QhGemmSeg seg = {w, s, o, N, kb};
-    const GemmPlan pl = gemm_plan(M, K, &seg, 1, cus, ws);
+    const GemmPlan pl = gemm_plan(M, K, &seg, 1, cus, ws, ws_bytes);
     if (pl.S > 1) {
       float* part = (float*)ws;
       if (scale_bf16) launch_gemm_plan<uint16_t>(pl, (const uint16_t*)x, &seg, 1, M, K, st, cus, part, false);
@@ -1051,21 +1051,21 @@ int qh_launch_gemm_e4m3_add_rmsnorm(const void* x, const void* w, const void* s,
       return 0;
     }
   }
-  if (qh_launch_gemm_e4m3_ws(x, w, s, o, M, N, K, kb, scale_bf16, ws, st) != 0) return -1;
+  if (qh_launch_gemm_e4m3_ws(x, w, s, o, M, N, K, kb, scale_bf16, ws, ws_bytes, st) != 0) return -1;
   if (norm_w) qh_launch_add_rmsnorm_rows(h, o, norm_w, hn, M, N, eps, st);
   else qh_launch_add_bf16(h, o, h, M * N, st);
   return 0;
 }
 
 int qh_launch_gemm_e4m3_ws(const void* x, const void* w, const void* s, void* y, int M, int N,
-                           int K, int kb, bool scale_bf16, void* ws, hipStream_t st) {
+                           int K, int kb, bool scale_bf16, void* ws, size_t ws_bytes, hipStream_t st) {
   const QhGemmSeg seg = {w, s, y, N, kb};
-  return qh_launch_gemm_e4m3_group_ws(x, M, K, &seg, 1, scale_bf16, ws, st);
+  return qh_launch_gemm_e4m3_group_ws(x, M, K, &seg, 1, scale_bf16, ws, ws_bytes, st);
 }
 
 // Without a caller workspace (the reference ABI passes none): no split-K and
 // nothing allocated.
 int qh_launch_gemm_e4m3(const void* x, const void* w, const void* s, void* y, int M, int N, int K,
                         int kb, bool scale_bf16, hipStream_t st) {
-  return qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scale_bf16, nullptr, st);
+  return qh_launch_gemm_e4m3_ws(x, w, s, y, M, N, K, kb, scale_bf16, nullptr, 0, st);
 }

@@ -819,7 +819,7 @@ bool rot_ok(int rot, int D) {
 }  // namespace
 
 int qh_launch_attn_prep(const QhAttnPrepParams& p, hipStream_t st) {
-  if ((p.D != 128 && p.D != 256) || !rot_ok(p.rot, p.D) || p.Hkv <= 0 || p.Hq % p.Hkv != 0 ||
+  if ((p.D != 128 && p.D != 256) || !rot_ok(p.rot, p.D) || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv != 0 ||
       p.past < 0 || p.past + p.M > p.max_seq) {
     qh_set_error("attn_prep: unsupported shape (D=%d rot=%d Hq=%d Hkv=%d past=%d M=%d max_seq=%d)",
                  p.D, p.rot, p.Hq, p.Hkv, p.past, p.M, p.max_seq);
@@ -835,7 +835,7 @@ int qh_launch_attn_prep(const QhAttnPrepParams& p, hipStream_t st) {
 }
 
 int qh_launch_attn_prefill(const QhAttnPrefillParams& p, hipStream_t st) {
-  if ((p.D != 128 && p.D != 256) || p.Hkv <= 0 || p.Hq % p.Hkv != 0 || p.Hq / p.Hkv > MAXG ||
+  if ((p.D != 128 && p.D != 256) || p.Hkv <= 0 || p.Hq <= 0 || p.Hq % p.Hkv != 0 || p.Hq / p.Hkv > MAXG ||
       p.past < 0 || p.past + p.M > p.max_seq) {
     qh_set_error("attn_prefill: unsupported shape (D=%d Hq=%d Hkv=%d past=%d M=%d)", p.D, p.Hq,
                  p.Hkv, p.past, p.M);
@@ -863,7 +863,7 @@ int qh_launch_attn_prefill(const QhAttnPrefillParams& p, hipStream_t st) {
 }
 
 int qh_launch_gdn_prep(const QhGdnPrepParams& p, hipStream_t st) {
-  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0 || p.Hv > 64 ||
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv <= 0 || p.Hv % p.Hk != 0 || p.Hv > 64 ||
       p.C != 2 * p.Hk * p.dk + p.Hv * p.dv || p.past < 0) {
     qh_set_error("gdn_prep: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d C=%d)", p.dk, p.dv, p.Hk,
                  p.Hv, p.C);
@@ -887,7 +887,7 @@ int qh_launch_gdn_prep(const QhGdnPrepParams& p, hipStream_t st) {
 }
 
 int qh_launch_gdn_scan(const QhGdnScanParams& p, hipStream_t st) {
-  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv % p.Hk != 0) {
+  if (p.dk != 128 || p.dv != 128 || p.Hk <= 0 || p.Hv <= 0 || p.Hv % p.Hk != 0) {
     qh_set_error("gdn_scan: unsupported shape (dk=%d dv=%d Hk=%d Hv=%d)", p.dk, p.dv, p.Hk, p.Hv);
     return -1;
   }

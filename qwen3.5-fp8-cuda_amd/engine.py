@@ -416,7 +416,7 @@ class Qwen35FP8Engine:
             abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(o), M, w.shape[0], w.shape[1],
             ops.scale_mode(w, s), int(s.dtype == torch.bfloat16), abi.ptr(h),
             abi.ptr(norm_w) if norm_w is not None else None, abi.ptr(hn), self.eps, abi.ptr(ws),
-            abi.stream_handle()), "gemm_add_rmsnorm")
+            ws.numel(), abi.stream_handle()), "gemm_add_rmsnorm")
 
     def _gemm_group(self, x, segs, M, ws):
         """Projections [((w, s), y), ...] of the same activation x in one
@@ -431,7 +431,7 @@ class Qwen35FP8Engine:
         w0, s0 = segs[0][0]
         abi.check(self.lib.qh_gemm_e4m3_grouped(abi.ptr(x), M, w0.shape[1], len(segs), *args,
                                                 int(s0.dtype == torch.bfloat16), abi.ptr(ws),
-                                                abi.stream_handle()), "gemm_grouped")
+                                                ws.numel(), abi.stream_handle()), "gemm_grouped")
 
     def prefill_batch(self, ids, past=0, keep=1, trace=None):
         """The reference's s > 1 prefill (main.py:1550-1566) of M tokens at

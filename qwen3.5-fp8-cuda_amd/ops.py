@@ -76,7 +76,7 @@ def fp8_linear(input_bf16, w_bytes, w_scale_inv, out=None):
             raise abi.QhError(err)
     else:
         abi.check(lib.qh_gemm_e4m3(abi.ptr(x2d), abi.ptr(w_bytes), abi.ptr(w_scale_inv),
-                                   abi.ptr(y), M, N, K, kb, 0, None, st), "fp8_linear")
+                                   abi.ptr(y), M, N, K, kb, 0, None, 0, st), "fp8_linear")
     return y.reshape(*orig[:-1], N)
 
 

@@ -78,14 +78,14 @@ def test_validation_errors_need_no_gpu():
     rc = lib.qh_add_rmsnorm(p, ctypes.c_void_p(8192), ctypes.c_void_p(12288), p, 4, 2560, 1e-6, None)
     assert rc == -1 and "alias" in abi.last_error()
     rc = lib.qh_gemm_e4m3_add_rmsnorm(None, None, None, None, 4, 2560, 100, 1, 0, None, None, None, 1e-6,
-                                      None, None)
+                                      None, 0, None)
     assert rc == -1 and "multiple of 128" in abi.last_error()
     rc = lib.qh_gemm_e4m3_add_rmsnorm(None, None, None, None, 4, 2560, 256, 2, 0, None, None, None, 1e-6,
-                                      None, None)
+                                      None, 0, None)
     assert rc == -1 and "null pointer" in abi.last_error()
     q = [ctypes.c_void_p(4096 * k) for k in range(1, 6)]
     rc = lib.qh_gemm_e4m3_add_rmsnorm(q[0], q[1], q[2], q[3], 4, 2560, 256, 2, 0, q[3], q[4], q[0], 1e-6,
-                                      None, None)
+                                      None, 0, None)
     assert rc == -1 and "distinct" in abi.last_error()
     rc = lib.qh_gated_rmsnorm(None, None, None, None, 4, 512, 1e-6, 1, None)
     assert rc == -1 and "head_dim" in abi.last_error()
@@ -105,6 +105,10 @@ def test_validation_errors_need_no_gpu():
     rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 64, 16, 32, 64, 128,
                           1e-6, None, 0, None)
     assert rc == -1 and "unsupported shape" in abi.last_error()
+    for Hk, Hv in [(16, 0), (16, -16), (0, 32)]:
+        rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, Hk, Hv, 128, 128,
+                              1e-6, ctypes.c_void_p(256), 1 << 30, None)
+        assert rc == -1 and "unsupported shape" in abi.last_error(), (Hk, Hv)
     need = int(lib.qh_gdn_chunk_workspace_size(130, 32))
     assert need == 32 * 3 * 99328
     rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, 16, 32, 128, 128,
@@ -113,19 +117,38 @@ def test_validation_errors_need_no_gpu():
     rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 130, 16, 32, 128, 128,
                           1e-6, ctypes.c_void_p(256), need - 1, None)
     assert rc == -1 and "workspace" in abi.last_error()
-    rc = lib.qh_gemm_e4m3(None, None, None, None, 4, 4, 100, 1, 0, None, None)
+    rc = lib.qh_gemm_e4m3(None, None, None, None, 4, 4, 100, 1, 0, None, 0, None)
     assert rc == -1
     # grouped GEMM: every check runs before anything touches a device pointer
     none4 = [None, None, None, 0, 0] * 4
-    rc = lib.qh_gemm_e4m3_grouped(None, 4, 2560, 1, *none4, 0, None, None)
+    rc = lib.qh_gemm_e4m3_grouped(None, 4, 2560, 1, *none4, 0, None, 0, None)
     assert rc == -1 and "null activation" in abi.last_error()
     fake = ctypes.c_void_p(256)
-    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 5, *none4, 0, fake, None)
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 5, *none4, 0, None, 0, None)
     assert rc == -1 and "nseg=5" in abi.last_error()
-    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 1, *none4, 0, fake, None)
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 2560, 1, *none4, 0, None, 0, None)
     assert rc == -1 and "segment 0" in abi.last_error()
-    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 100, 1, *none4, 0, fake, None)
+    rc = lib.qh_gemm_e4m3_grouped(fake, 4, 100, 1, *none4, 0, None, 0, None)
     assert rc == -1
+    # split-K workspace: a buffer smaller than qh_gemm_workspace_size, or
+    # misaligned, is refused before anything touches the device
+    need = int(lib.qh_gemm_workspace_size(512, 2560))
+    assert need == 16 << 20
+    ws = ctypes.c_void_p(1 << 20)
+    x4 = [ctypes.c_void_p(4096 * k) for k in range(1, 5)]
+    for nbytes, addr, msg in [(need - 1, ws, "smaller than"), (0, ws, "smaller than"),
+                              (need, ctypes.c_void_p((1 << 20) + 16), "256-byte aligned")]:
+        lib.qh_clear_error()
+        rc = lib.qh_gemm_e4m3(*x4, 512, 9216, 2560, 20, 0, addr, nbytes, None)
+        assert rc == -1 and msg in abi.last_error(), abi.last_error()
+        lib.qh_clear_error()
+        rc = lib.qh_gemm_e4m3_grouped(x4[0], 512, 2560, 1, x4[1], x4[2], x4[3], 9216, 20,
+                                      *([None, None, None, 0, 0] * 3), 0, addr, nbytes, None)
+        assert rc == -1 and msg in abi.last_error(), abi.last_error()
+        lib.qh_clear_error()
+        rc = lib.qh_gemm_e4m3_add_rmsnorm(x4[0], x4[1], x4[2], x4[3], 512, 2560, 9216, 72, 0,
+                                          ctypes.c_void_p(1 << 24), None, None, 1e-6, addr, nbytes, None)
+        assert rc == -1 and msg in abi.last_error(), abi.last_error()
     # reference symbols: no error channel in the reference; ours records one
     lib.qh_clear_error()
     lib.launch_gemv_v4_extern(None, None, None, None, 16, 12, 1, None)

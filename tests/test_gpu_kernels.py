@@ -283,9 +283,21 @@ def _attn_case(g, ctx, Hq=16, Hkv=4, D=256, rot=64, max_seq=None):
 def test_attn_decode(ctx, splits):
     """BASELINE config 4b (ctx 4096): q/k norm, partial RoPE (theta 1e7, 64 of
     256 dims), KV write at slot ctx-1, GQA 16/4, sigmoid gate."""
-    g = gen(ctx)
-    Hq, Hkv, D, rot, max_seq = 16, 4, 256, 64, 4096
-    kc, vc, q_all, k_new, v_new, qn, kn = _attn_case(g, ctx, max_seq=max_seq)
+    _check_attn_decode(ctx, splits, 16, 4)
+
+
+# Groups of 5..8 query heads per KV head run the two-heads-per-wave form of
+# the kernel (a wave holds two query heads' q and P.V accumulators).
+@pytest.mark.parametrize("Hq,Hkv,ctx,splits", [(8, 1, 700, 16), (16, 2, 4096, 64), (6, 1, 300, 8),
+                                               (12, 2, 129, 4), (5, 1, 33, 2)])
+def test_attn_decode_group_sizes(Hq, Hkv, ctx, splits):
+    _check_attn_decode(ctx, splits, Hq, Hkv)
+
+
+def _check_attn_decode(ctx, splits, Hq, Hkv):
+    g = gen(ctx + 1000 * Hq + Hkv)
+    D, rot, max_seq = 256, 64, 4096
+    kc, vc, q_all, k_new, v_new, qn, kn = _attn_case(g, ctx, Hq=Hq, Hkv=Hkv, max_seq=max_seq)
     # Cache rows past the context hold NaN: no split may read a row it does
     # not own into the result.
     kc[:, ctx:] = float("nan")
@@ -314,7 +326,8 @@ def test_attn_decode(ctx, splits):
                                      abi.ptr(scratch), abi.ptr(counters), abi.ptr(out), 1e-6,
                                      abi.stream_handle()))
         sync()
-        assert_close(out, ref, atol_frac=1e-3, what=f"attn ctx={ctx} splits={splits} dev_pos={use_dev_pos}")
+        assert_close(out, ref, atol_frac=1e-3,
+                     what=f"attn {Hq}/{Hkv} ctx={ctx} splits={splits} dev_pos={use_dev_pos}")
         assert torch.equal(kcg[:, pos].cpu().float(), kc_ref[:, pos]), "K cache slot"
         assert torch.equal(vcg[:, pos].cpu().float(), vc_ref[:, pos]), "V cache slot"
         assert int(counters.abs().sum()) == 0, "arrival counters must self-reset"
@@ -602,7 +615,7 @@ def test_gemm_e4m3(M, N, K):
     ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
     yw = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     abi.check(lib.qh_gemm_e4m3(abi.ptr(cu(x)), abi.ptr(cu(w)), abi.ptr(cu(s)), abi.ptr(yw), M, N, K,
-                               K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm with workspace")
+                               K // 128, 0, abi.ptr(ws), ws.numel(), abi.stream_handle()), "gemm with workspace")
     sync()
     assert cos_sim(yw.cpu().float(), ref) >= 0.99999
     assert_close(yw, orc.bf16(ref), rtol=2e-2, atol_frac=5e-3, min_cos=0.99999, what="gemm, workspace")
@@ -631,7 +644,7 @@ def test_gemm_add_rmsnorm_matches_separate_steps(M, N, K, norm):
     h1 = cu(h0)
     hn1 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     abi.check(lib.qh_gemm_e4m3(abi.ptr(dx), abi.ptr(dw), abi.ptr(ds), abi.ptr(o1), M, N, K, K // 128, 0,
-                               abi.ptr(ws), abi.stream_handle()), "gemm")
+                               abi.ptr(ws), ws.numel(), abi.stream_handle()), "gemm")
     if norm:
         abi.check(lib.qh_add_rmsnorm(abi.ptr(h1), abi.ptr(o1), abi.ptr(dnw), abi.ptr(hn1), M, N, 1e-6,
                                      abi.stream_handle()), "add_rmsnorm")
@@ -643,7 +656,7 @@ def test_gemm_add_rmsnorm_matches_separate_steps(M, N, K, norm):
     hn2 = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
     abi.check(lib.qh_gemm_e4m3_add_rmsnorm(abi.ptr(dx), abi.ptr(dw), abi.ptr(ds), abi.ptr(o2), M, N, K,
                                            K // 128, 0, abi.ptr(h2), abi.ptr(dnw) if norm else None,
-                                           abi.ptr(hn2), 1e-6, abi.ptr(ws), abi.stream_handle()),
+                                           abi.ptr(hn2), 1e-6, abi.ptr(ws), ws.numel(), abi.stream_handle()),
               "gemm_add_rmsnorm")
     sync()
     assert torch.equal(h1.cpu(), h2.cpu()), "residual stream differs from the separate steps"
@@ -672,7 +685,7 @@ def test_gemm_grouped_matches_single_launches(M):
     args = []
     for (w, s), y, n in zip(dw, yg, ns):
         args += [abi.ptr(w), abi.ptr(s), abi.ptr(y), n, ops.scale_mode(w, s)]
-    abi.check(lib.qh_gemm_e4m3_grouped(abi.ptr(dx), M, K, 4, *args, 0, abi.ptr(ws),
+    abi.check(lib.qh_gemm_e4m3_grouped(abi.ptr(dx), M, K, 4, *args, 0, abi.ptr(ws), ws.numel(),
                                        abi.stream_handle()), "grouped")
     ys = [ops.fp8_linear(dx, w, s) for w, s in dw]
     sync()
@@ -751,7 +764,7 @@ def test_gemm_activation_outlier_channels(path):
     else:
         ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device=DEV)
         abi.check(lib.qh_gemm_e4m3(abi.ptr(dx), abi.ptr(dw), abi.ptr(cu(s)), abi.ptr(y), M, N, K,
-                                   K // 128, 0, abi.ptr(ws), abi.stream_handle()), "gemm")
+                                   K // 128, 0, abi.ptr(ws), ws.numel(), abi.stream_handle()), "gemm")
     sync()
     assert abi.last_error() == ""
     c = cos_sim(y.cpu().float(), ref)

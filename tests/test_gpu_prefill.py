@@ -83,14 +83,16 @@ def test_attention_prefill(M, past, Hq, Hkv, D):
 # filled ring and state: the conv reads positions before the prompt.
 # algo "chunk" (qh_gdn_chunk): M = 64 one full chunk, 130 two chunks and a
 # 2-token tail, 200 from a stored state over four chunks, 600 (from a stored
-# state) the 8-channel conv kernel of prompts of 512+ tokens.
-@pytest.mark.parametrize("M,past,algo", [(45, 0, "scan"), (3, 0, "scan"), (8, 6, "scan"),
-                                         (21, 6, "scan"), (45, 0, "chunk"), (3, 0, "chunk"),
-                                         (21, 6, "chunk"), (64, 0, "chunk"), (130, 0, "chunk"),
-                                         (200, 6, "chunk"), (600, 6, "chunk")])
-def test_gdn_prefill(M, past, algo):
-    g = gen(22 + M + past)
-    Hk, Hv, dk, dv = 2, 4, 128, 128
+# state) the 8-channel conv kernel of prompts of 512+ tokens.  Hv = 8 and 32
+# (Hv % 8 == 0) place the state kernel's 8 workgroups of a head on one XCD.
+@pytest.mark.parametrize("M,past,algo,Hk,Hv", [
+    (45, 0, "scan", 2, 4), (3, 0, "scan", 2, 4), (8, 6, "scan", 2, 4), (21, 6, "scan", 2, 4),
+    (45, 0, "chunk", 2, 4), (3, 0, "chunk", 2, 4), (21, 6, "chunk", 2, 4), (64, 0, "chunk", 2, 4),
+    (130, 0, "chunk", 2, 4), (200, 6, "chunk", 2, 4), (600, 6, "chunk", 2, 4),
+    (130, 6, "chunk", 4, 8), (70, 6, "chunk", 16, 32), (130, 0, "scan", 16, 32)])
+def test_gdn_prefill(M, past, algo, Hk, Hv):
+    g = gen(22 + M + past + Hv)
+    dk, dv = 128, 128
     C = 2 * Hk * dk + Hv * dv
     mixed = bf(randn(g, M, C))
     a, b = bf(randn(g, M, Hv)), bf(randn(g, M, Hv))
