@@ -55,6 +55,20 @@ def log(msg):
 REFERENCE_TOKS = 53.9            # README.md:50-52 (RTX 5060, real checkpoint)
 
 
+def decode_bytes_per_token(w, cfg, ctx):
+    """HBM bytes one decode step at context `ctx` must move: the
+    E4M3 linears with their scales, the bf16 lm_head and one embedding row
+    (w.nbytes_per_token()), every GatedDeltaNet layer's fp32 recurrent state
+    and bf16 conv state read and written, and every attention layer's K and V
+    rows of the context read."""
+    n_full = sum(1 for i in range(cfg.num_hidden_layers) if cfg.is_full(i))
+    n_gdn = cfg.num_hidden_layers - n_full
+    state = cfg.linear_num_value_heads * cfg.linear_key_head_dim * cfg.linear_value_head_dim * 4
+    conv = cfg.conv_dim * cfg.linear_conv_kernel_dim * 2
+    kv = 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * ctx
+    return w.nbytes_per_token() + n_gdn * 2 * (state + conv) + n_full * kv
+
+
 def mlp_bytes(cfg):
     H, I = cfg.hidden_size, cfg.intermediate_size
     w = 2 * I * H                                  # gate + up E4M3 bytes
@@ -491,10 +505,14 @@ def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
     own free-running greedy tokens from the same prompt are compared with the
     oracle's.  The oracle stops early once budget_s seconds have passed.  The
     first n_timed oracle decode steps are the CPU baseline sample."""
+    from oracle import parity_floor
     from oracle import qwen35_oracle as orc
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     t0 = time.perf_counter()
     ref = orc.OracleModel(w_cpu, max_seq_len=len(prompt) + n_steps + 1, prefill="reference")
+    # the RoPE tables the engine built on the device (as main.py:513-533 does)
+    ref.cos = eng.rope_cos[:ref.max_seq_len].cpu()
+    ref.sin = eng.rope_sin[:ref.max_seq_len].cpu()
     setup = time.perf_counter() - t0
     log(f"cpu oracle ready ({setup:.0f} s)")
     # GPU free-running greedy tokens from the same prompt
@@ -537,6 +555,15 @@ def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
     first_diff = next((i for i in range(n) if g_free[i] != o_toks[i]), None)
     decided = [r for r in rows if r[1]]
     timed = step_s[:n_timed]
+    gpu = parity_floor.summarize([r[0] for r in rows], [r[2] for r in rows], [r[4] for r in rows])
+    try:
+        fx = parity_floor.load()
+        floor = {k: {kk: vv for kk, vv in v.items() if kk != "disagreements_row_margin_ulps"}
+                 for k, v in parity_floor.floor_summaries(fx, rows=len(rows)).items()}
+        floor["source"] = "tests/golden/config5_noise_floor.json (tests/golden/make_noise_floor.py)"
+        floor["same_oracle_tokens_as_fixture"] = o_toks[:len(rows)] == fx["fp32_greedy_tokens"][:len(rows)]
+    except (OSError, ValueError, KeyError) as e:
+        floor = {"error": f"no noise-floor fixture: {e}"}
     out = {
         "prompt_tokens": len(prompt), "steps": n, "requested_steps": n_steps,
         "free_running_identical_steps": n if first_diff is None else first_diff,
@@ -553,11 +580,10 @@ def parity_run(eng, w_cpu, prompt, n_steps, budget_s, n_timed=32):
             "disagreements": [{"position": i, "margin": round(r[3], 6),
                                "margin_bf16_ulps": round(r[4], 2)}
                               for i, r in enumerate(rows) if not r[2]],
-            "noise_floor": "two exact restatements of the reference (oracle fp32 vs fp64-accumulated "
-                           "matmuls, tests/parity_noise_floor.py, 60 positions of this model) agree "
-                           "at 52/54 positions above 1 ulp, mean logit cosine 0.99943, disagreeing "
-                           "only at margins <= 2 ulps",
+            "window_min_logit_cosine": [round(c, 7) for c in gpu["window_min_logit_cosine"]],
+            "largest_disagreeing_margin_ulps": gpu["largest_disagreeing_margin_ulps"],
         },
+        "noise_floor": floor,
         "oracle": "CPU explicit-dequant restatement (oracle/qwen35_oracle.py), batch prefill path",
         "oracle_prefill_s": round(prefill_s, 1),
         "oracle_decode_s_per_token": round(sum(step_s) / max(1, len(step_s)), 3),
@@ -666,7 +692,9 @@ def main():
     log(f"timed decode: {toks_per_s:.1f} tok/s; memory {mem}")
     ms_per_step = dt * 1e3 / args.steps
     ctx0 = args.prompt + args.warmup
-    bytes_tok = w.nbytes_per_token()
+    # mean over the timed steps (contexts ctx0 + 1 .. ctx0 + steps)
+    bytes_tok = round(sum(decode_bytes_per_token(w, cfg, ctx0 + 1 + k) for k in range(args.steps))
+                      / args.steps)
 
     floor = launch_floor()
     log(f"launch floor: {floor['empty_kernel_us']} us empty kernel, {floor['gemv_128x2560_us']} us "
@@ -716,8 +744,13 @@ def main():
                         "GQA attention), batch 1, greedy decode, HIP-graph replay per token",
             "prompt_tokens": args.prompt,
             "decode_context": [ctx0, ctx0 + args.steps],
-            "weight_bytes_per_token": bytes_tok,
+            "bytes_per_token": bytes_tok,
+            "bytes_per_token_counts": "E4M3 linears + scales, bf16 lm_head, one embedding row, "
+                                      "GatedDeltaNet recurrent + conv state read and written, K/V "
+                                      "of the context read (mean over the timed steps)",
+            "weight_bytes_per_token": w.nbytes_per_token(),
             "effective_GBps": round(bytes_tok * toks_per_s / 1e9, 1),
+            "hbm_roofline_frac_per_token": round(bytes_tok * toks_per_s / 1e9 / HBM_PEAK_GBS, 4),
             "parallelism": "single GPU",
             "baseline": "reference README 53.9 tok/s on RTX 5060 (different GPU, real checkpoint)",
         },

@@ -29,10 +29,22 @@ import torch.nn.functional as F
 
 BLOCK = 128
 
+# Arithmetic type of the model path: float32 (the oracle every test compares
+# with) or float64 (the exact path: every intermediate in double precision,
+# rounded to bf16 only where the reference materialises a bf16 tensor; with
+# MATMUL = "fp64" below).  Only the noise-floor fixture generator
+# (tests/golden/make_noise_floor.py) sets float64.
+ACC = torch.float32
+
+
+def _a(x):
+    """x in the model path's arithmetic type (ACC)."""
+    return x.to(ACC)
+
 
 def bf16(x):
-    """Materialise as bf16 (RNE) and come back to fp32."""
-    return x.to(torch.bfloat16).float()
+    """Materialise as bf16 (RNE) and come back to the arithmetic type (fp32)."""
+    return x.to(torch.bfloat16).to(ACC)
 
 
 # ---------------------------------------------------------------- A0: E4M3FN
@@ -96,9 +108,37 @@ def dequant(w_u8, s, code=None):
     return W * full
 
 
+# How the weight products accumulate.  "fp32": one fp32 matmul (what every
+# test compares with).  "fp64": fp64 accumulation of the same fp32 operands.
+# "kblock": fp32 partial sums per 128-wide K block, added block by block in
+# fp32 (the order of the reference's block-scaled kernels, fused_kernels.cu:
+# 127-145).  Only the noise-floor fixture generator
+# (tests/golden/make_noise_floor.py) sets anything but "fp32": three exact
+# restatements of the same path that differ only in rounding.
+MATMUL = "fp32"
+
+
+def wmm(x, W):
+    """x @ W^T (x [..., K], W [N, K] fp32), accumulated as MATMUL says; fp32."""
+    if MATMUL == "fp32":
+        return _a(x.float() @ W.t())
+    if MATMUL == "fp64":
+        xd = x.double()
+        parts = [_a(xd @ W[n0:n0 + 8192].double().t()) for n0 in range(0, W.shape[0], 8192)]
+        return torch.cat(parts, dim=-1)
+    if MATMUL == "kblock":
+        x = x.float()
+        out = None
+        for k0 in range(0, x.shape[-1], BLOCK):
+            p = x[..., k0:k0 + BLOCK] @ W[:, k0:k0 + BLOCK].t()
+            out = p if out is None else out + p
+        return _a(out)
+    raise ValueError(f"unknown MATMUL mode {MATMUL!r}")
+
+
 def linear(x, W):
     """bf16(x @ W^T) with fp32 accumulation (fp8_linear / F.linear output)."""
-    return bf16(x.float() @ W.t())
+    return bf16(wmm(x, W))
 
 
 def gemv_fp64(x, w_u8, s):
@@ -109,19 +149,19 @@ def gemv_fp64(x, w_u8, s):
 # ------------------------------------------------------------ A3 RMSNorm
 def rmsnorm(x, w, eps=1e-6):
     """(1+w) RMSNorm, bf16 output (main.py:921-924, fused_kernels.cu:540-546)."""
-    x = x.float()
+    x = _a(x)
     r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
-    return bf16((x * r) * (1.0 + w.float()))
+    return bf16((x * r) * (1.0 + _a(w)))
 
 
 # --------------------------------------------------------------- A2 MLP
 def mlp_decode(h, o, ln_w, Wg, Wu, Wd, eps=1e-6):
     """layer_post_o_fp8_mlp (fused_kernels.cu:1156-1195): h2 = bf16(h + o);
     SiLU on the fp32 gate/up accumulators (fused_kernels.cu:476)."""
-    h2 = bf16(h.float() + o.float())
+    h2 = bf16(_a(h) + _a(o))
     xn = rmsnorm(h2, ln_w, eps)
-    g = xn @ Wg.t()
-    u = xn @ Wu.t()
+    g = wmm(xn, Wg)
+    u = wmm(xn, Wu)
     m = bf16(F.silu(g) * u)
     d = linear(m, Wd)
     return bf16(h2 + d), m
@@ -150,7 +190,7 @@ def rope_rows(x, cos_row, sin_row, rot, round_out):
     """Partial RoPE on dims [0, rot) of each row: pairs (c, c + rot/2)
     (fused_kernels.cu:872-903 decode, main.py:964-976 prefill)."""
     half = rot // 2
-    x = x.float()
+    x = _a(x)
     x0, x1 = x[..., :half], x[..., half:rot]
     c0, c1 = cos_row[..., :half], cos_row[..., half:rot]
     s0, s1 = sin_row[..., :half], sin_row[..., half:rot]
@@ -164,8 +204,8 @@ def rope_rows(x, cos_row, sin_row, rot, round_out):
 def attn_core(q, K, V):
     """softmax(q K^T / sqrt(D)) V in fp32 for one head; q [D] or [s, D]."""
     D = q.shape[-1]
-    sc = (q.float() @ K.float().t()) * (1.0 / math.sqrt(D))
-    return torch.softmax(sc, dim=-1) @ V.float()
+    sc = (_a(q) @ _a(K).t()) * (1.0 / math.sqrt(D))
+    return torch.softmax(sc, dim=-1) @ _a(V)
 
 
 def attn_decode(q_all, k_new, v_new, q_norm, k_norm, cos, sin, k_cache, v_cache, pos, n_heads,
@@ -174,15 +214,15 @@ def attn_decode(q_all, k_new, v_new, q_norm, k_norm, cos, sin, k_cache, v_cache,
     q_all: [n_heads * 2 * D] with per-head [q | gate]; caches [n_kv, max_seq, D]
     (updated in place).  Returns the gated bf16 output [n_heads * D]."""
     D = head_dim
-    qa = q_all.float().view(n_heads, 2 * D)
+    qa = _a(q_all).view(n_heads, 2 * D)
     q, gate = qa[:, :D], qa[:, D:]
     q = rmsnorm(q, q_norm, eps) if q_norm is not None else q
-    k = rmsnorm(k_new.float().view(n_kv, D), k_norm, eps) if k_norm is not None else k_new.float().view(n_kv, D)
+    k = rmsnorm(_a(k_new).view(n_kv, D), k_norm, eps) if k_norm is not None else _a(k_new).view(n_kv, D)
     q = rope_rows(q, cos[pos], sin[pos], rot, round_out=True)
     k = rope_rows(k, cos[pos], sin[pos], rot, round_out=True)
     k_cache[:, pos] = k
-    v_cache[:, pos] = v_new.float().view(n_kv, D)
-    out = torch.empty(n_heads, D)
+    v_cache[:, pos] = _a(v_new).view(n_kv, D)
+    out = torch.empty(n_heads, D, dtype=ACC)
     for h in range(n_heads):
         kv = h * n_kv // n_heads
         out[h] = bf16(attn_core(q[h], k_cache[kv, :pos + 1], v_cache[kv, :pos + 1]))
@@ -210,16 +250,16 @@ def conv_update(x, state, w):
     """transformers causal_conv1d_update (modeling_qwen3_5.py:200-217) for one
     token: window = [state | x], state <- last 4, y = bf16(silu(bf16(conv))).
     x [C], state [C, 4] ordered oldest..newest (updated in place), w [C, 4]."""
-    win = torch.cat([state.float(), x.float().view(-1, 1)], dim=1)
+    win = torch.cat([_a(state), _a(x).view(-1, 1)], dim=1)
     state.copy_(win[:, 1:])
-    y = bf16((w.float() * win[:, 1:]).sum(dim=1))
+    y = bf16((_a(w) * win[:, 1:]).sum(dim=1))
     return bf16(F.silu(y))
 
 
 def linear_gates(a, b, A_log, dt_bias):
     """beta = bf16(sigmoid(b)); g = -exp(A_log) * softplus(a + dt_bias) (main.py:1120-1122)."""
-    beta = bf16(torch.sigmoid(b.float()))
-    g = -torch.exp(A_log.float()) * softplus(a.float() + dt_bias.float())
+    beta = bf16(torch.sigmoid(_a(b)))
+    g = -torch.exp(_a(A_log)) * softplus(_a(a) + _a(dt_bias))
     return g, beta
 
 
@@ -227,14 +267,14 @@ def delta_rule_step(q, k, v, g, beta, S):
     """launch_delta_rule_decode (fused_kernels.cu:623-684): fp32 l2norm of q and
     k (eps inside the rsqrt of the sum), q scaled by 1/sqrt(dk); S [H, dk, dv]
     updated in place; returns bf16 o [H, dv]."""
-    q, k, v = q.float(), k.float(), v.float()
+    q, k, v = _a(q), _a(k), _a(v)
     dk = q.shape[-1]
     qn = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6) * (1.0 / math.sqrt(dk))
     kn = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
-    decay = torch.exp(g.float()).view(-1, 1, 1)
+    decay = torch.exp(_a(g)).view(-1, 1, 1)
     Sd = S * decay
     pred = (Sd * kn.unsqueeze(-1)).sum(dim=-2)
-    delta = (v - pred) * beta.float().view(-1, 1)
+    delta = (v - pred) * _a(beta).view(-1, 1)
     S.copy_(Sd + kn.unsqueeze(-1) * delta.unsqueeze(-2))
     return bf16((S * qn.unsqueeze(-1)).sum(dim=-2))
 
@@ -242,12 +282,12 @@ def delta_rule_step(q, k, v, g, beta, S):
 def gated_rmsnorm(core, z, w, eps=1e-6, bf16_steps=True):
     """Per head [H, dv]: main.py:1152-1158 (bf16_steps) or the fused kernel
     fused_kernels.cu:592-618 (fp32 throughout)."""
-    c = core.float()
+    c = _a(core)
     r = torch.rsqrt(c.pow(2).mean(-1, keepdim=True) + eps)
     if bf16_steps:
-        normed = bf16(bf16(c * r) * w.float())
-        return bf16(normed * bf16(F.silu(z.float())))
-    return bf16(c * r * w.float() * F.silu(z.float()))
+        normed = bf16(bf16(c * r) * _a(w))
+        return bf16(normed * bf16(F.silu(_a(z))))
+    return bf16(c * r * _a(w) * F.silu(_a(z)))
 
 
 def l2norm_bf16(x, eps=1e-6):
@@ -264,7 +304,7 @@ def gated_delta_rule_seq(q, k, v, g, beta, S):
     normalised, q already scaled.  q,k [T, H, dk], v [T, H, dv], g/beta [T, H];
     S [H, dk, dv] updated in place; returns fp32 o [T, H, dv]."""
     T = q.shape[0]
-    out = torch.empty(T, q.shape[1], v.shape[-1])
+    out = torch.empty(T, q.shape[1], v.shape[-1], dtype=ACC)
     for t in range(T):
         S.mul_(torch.exp(g[t]).view(-1, 1, 1))
         mem = (S * k[t].unsqueeze(-1)).sum(dim=-2)
@@ -412,17 +452,17 @@ class OracleModel:
         for i in range(cfg.num_hidden_layers):
             if cfg.is_full(i):
                 shp = (cfg.num_key_value_heads, self.max_seq_len, cfg.head_dim)
-                self.k_cache.append(torch.zeros(shp))
-                self.v_cache.append(torch.zeros(shp))
+                self.k_cache.append(torch.zeros(shp, dtype=ACC))
+                self.v_cache.append(torch.zeros(shp, dtype=ACC))
                 self.conv_state.append(None)
                 self.rec_state.append(None)
             else:
                 self.k_cache.append(None)
                 self.v_cache.append(None)
-                self.conv_state.append(torch.zeros(cfg.conv_dim, cfg.linear_conv_kernel_dim))
+                self.conv_state.append(torch.zeros(cfg.conv_dim, cfg.linear_conv_kernel_dim, dtype=ACC))
                 self.rec_state.append(torch.zeros(cfg.linear_num_value_heads,
                                                   cfg.linear_key_head_dim,
-                                                  cfg.linear_value_head_dim))
+                                                  cfg.linear_value_head_dim, dtype=ACC))
 
     # ---- decode (s == 1) ---------------------------------------------------
     def _full_decode(self, i, hn, pos):
@@ -456,7 +496,7 @@ class OracleModel:
         """One decode step (main.py:1509-1547); with a list `trace`, the hidden
         state after every layer is appended to it."""
         cfg = self.cfg
-        h = self.embed[tok].clone()
+        h = _a(self.embed[tok])
         for i in range(cfg.num_hidden_layers):
             ly = self.layers[i]
             hn = rmsnorm(h, ly["input_layernorm"], self.eps)
@@ -485,7 +525,7 @@ class OracleModel:
         self.k_cache[i][:, past:past + s] = bf16(k).transpose(0, 1)
         self.v_cache[i][:, past:past + s] = v.transpose(0, 1)
         total = past + s
-        out = torch.empty(s, Hq, D)
+        out = torch.empty(s, Hq, D, dtype=ACC)
         mask = torch.triu(torch.full((s, total), float("-inf")), diagonal=1 + past)
         for h in range(Hq):
             kv = h * Hkv // Hq
@@ -527,7 +567,7 @@ class OracleModel:
         the greedy token after the last one.  With a list `trace`, the last
         token's hidden state after every layer is appended to it."""
         cfg = self.cfg
-        h = self.embed[ids]
+        h = _a(self.embed[ids])
         for i in range(cfg.num_hidden_layers):
             ly = self.layers[i]
             hn = rmsnorm(h, ly["input_layernorm"], self.eps)

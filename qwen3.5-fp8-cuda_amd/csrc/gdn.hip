@@ -166,8 +166,8 @@ __global__ __launch_bounds__(GDN_THREADS) void gdn_decode_kernel(QhGdnParams p) 
   }
   // ---- gates ----------------------------------------------------------------
   const float beta = rbf(qh_sigmoid(bh));
-  const float g = -__expf(A_log) * qh_softplus(ah + dt_bias);
-  const float decay = __expf(g);
+  const float g = -expf(A_log) * qh_softplus(ah + dt_bias);
+  const float decay = expf(g);
   __syncthreads();
 
   // ---- delta rule on column j ---------------------------------------------
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(64) void gdn_decode_cols_kernel(QhGdnParams p) {
   *(qh_f32x2*)(sq + 2 * lane) = qh_f32x2{q0 * iq, q1 * iq};
   *(qh_f32x2*)(sk + 2 * lane) = qh_f32x2{k0 * ik, k1 * ik};
   const float beta = rbf(qh_sigmoid(bh));
-  const float decay = __expf(-__expf(A_log) * qh_softplus(ah + dt_bias));
+  const float decay = expf(-expf(A_log) * qh_softplus(ah + dt_bias));
   __syncthreads();  // one wave: orders the LDS writes before the reads
   float kr[RPT], qr[RPT];
 #pragma unroll
@@ -346,7 +346,7 @@ __global__ __launch_bounds__(256) void delta_rule_kernel(const uint16_t* q, cons
       if (i0 + e < DK) (is_k ? kn : qn)[i0 + e] = vals[e] * sc;
   }
   __syncthreads();
-  const float decay = __expf(g[h]);
+  const float decay = expf(g[h]);
   const float bt = bf2f(beta[h]);
   const int j = tid & 31;
   const float vval = bf2f(v[(size_t)h * DK + sidx * VS + j]);

@@ -35,7 +35,6 @@ namespace {
 // (checked by the launchers) so that kOob plus any folded immediate offset stays
 // out of range.
 constexpr uint32_t kOob = 0x80000000u;
-constexpr uint32_t kMaxBufferRange = 0x7fffffffu;
 typedef __amdgpu_buffer_rsrc_t qh_rsrc;
 
 __device__ __forceinline__ qh_rsrc make_rsrc(const void* p, uint32_t bytes) {
@@ -157,7 +156,7 @@ __device__ __forceinline__ void block_x_load(XIn<CPL, NT>& in, const uint16_t* x
 // Gated RMSNorm of one element with the reference's bf16 intermediates
 // (main.py:1152-1158): bf16(bf16(c * rs) * w) * bf16(silu(z)), then bf16.
 __device__ __forceinline__ float gated1(float c, float z, float rs, float w) {
-  return rbf(rbf(c * rs) * w) * rbf(qh_silu(z));
+  return rbf(rbf(c * rs) * w) * rbf(qh_silu_fast(z));
 }
 __device__ __forceinline__ u32x4 gated_bf16x8(u32x4 c, u32x4 z, float rs, u32x4 w) {
   u32x4 r;

@@ -38,7 +38,7 @@ __global__ void linear_gates_kernel(const uint16_t* a, const uint16_t* b, const 
                                     int heads) {
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= heads) return;
-  g_out[h] = -__expf(A_log[h]) * qh_softplus(bf2f(a[h]) + dt_bias[h]);
+  g_out[h] = -expf(A_log[h]) * qh_softplus(bf2f(a[h]) + dt_bias[h]);
   beta_out[h] = f2bf(qh_sigmoid(bf2f(b[h])));
 }
 

@@ -321,7 +321,6 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(QhAttnPrefillPar
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int head = kvh * 4 + wid;
-  const int tok = min(m0 + r, p.M - 1);  // this lane's query (clamped for the loads)
   const int qpos = p.past + m0 + r;      // its position
   const int kv_end = p.past + min(m0 + 32, p.M);
   const int q0pos = p.past + m0;         // the workgroup's first query position
@@ -602,7 +601,7 @@ __global__ __launch_bounds__(256) void gdn_norm_gates_kernel(QhGdnPrepParams p) 
   } else if (lane < p.Hv) {
     const int h = lane;
     const float a = bf2f(p.a[(size_t)m * p.Hv + h]), b = bf2f(p.b[(size_t)m * p.Hv + h]);
-    p.g[(size_t)m * p.Hv + h] = -__expf(p.A_log[h]) * qh_softplus(a + p.dt_bias[h]);
+    p.g[(size_t)m * p.Hv + h] = -expf(p.A_log[h]) * qh_softplus(a + p.dt_bias[h]);
     p.beta[(size_t)m * p.Hv + h] = f2bf(qh_sigmoid(b));
   }
 }
@@ -663,7 +662,7 @@ __global__ __launch_bounds__(64) void gdn_scan_kernel(QhGdnScanParams p) {
     float* ks = sk[d & 1];
     *(qh_f32x2*)(qs + 2 * lane) = qh_f32x2{bf_lo(qq[d]) * qscale, bf_hi(qq[d]) * qscale};
     *(qh_f32x2*)(ks + 2 * lane) = qh_f32x2{bf_lo(kk[d]), bf_hi(kk[d])};
-    const float v = bf2f(vv[d]), decay = __expf(gg[d]), beta = bf2f(bb[d]);
+    const float v = bf2f(vv[d]), decay = expf(gg[d]), beta = bf2f(bb[d]);
     fetch(m + A, d);
     __syncthreads();  // one wave: orders the LDS writes before the reads
     float kr[RPT], qr[RPT];

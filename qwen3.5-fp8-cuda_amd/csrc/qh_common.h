@@ -203,11 +203,18 @@ __device__ __forceinline__ void reset_counter(unsigned* counter) {
 }
 
 // ---- math --------------------------------------------------------------------
-__device__ __forceinline__ float qh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float qh_silu(float x) { return x / (1.0f + __expf(-x)); }
+// The logistic functions use the accurate exponential (expf, about one ulp):
+// their results feed bf16 roundings and the GatedDeltaNet recurrent state,
+// where the fast hardware exponential's larger error shows up as rounding
+// flips and a per-step bias against the reference's fp32 torch ops.
+__device__ __forceinline__ float qh_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float qh_silu(float x) { return x / (1.0f + expf(-x)); }
+// SiLU on the fast exponential, for per-element loops on a kernel's critical
+// path (the gated RMSNorm prologue of the decode output projection).
+__device__ __forceinline__ float qh_silu_fast(float x) { return x / (1.0f + __expf(-x)); }
 // torch.nn.functional.softplus(beta=1, threshold=20)
 __device__ __forceinline__ float qh_softplus(float x) {
-  return x > 20.0f ? x : log1pf(__expf(x));
+  return x > 20.0f ? x : log1pf(expf(x));
 }
 
 // ---- scale addressing ----------------------------------------------------
