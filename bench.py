@@ -473,6 +473,51 @@ def launch_floor():
             "timing": "HIP graph of 64 launches replayed 20 times between HIP events"}
 
 
+# (label, bytes): the weight bytes of each decode kernel class (SURVEY 8d shapes)
+READ_FLOOR_SIZES = [("o_proj / out_proj 2560x4096", 2560 * 4096), ("down 2560x9216", 2560 * 9216),
+                    ("qkv 10240x2560", 10240 * 2560), ("in_proj 12352x2560", 12352 * 2560),
+                    ("gate/up 2 x 9216x2560", 2 * 9216 * 2560)]
+
+
+def read_floor(eng, pool_mib=640):
+    """What one launch can read: qh_read_stream (16-byte non-temporal loads,
+    each wave streaming a contiguous share, no arithmetic to speak of) over the
+    bytes of each decode kernel class, rotating over disjoint slices of a
+    `pool_mib` MiB buffer (more than the 256 MB MALL) in a HIP graph, and over
+    the lm_head's own 1.27 GB weight; the best of 1-4 workgroups per CU.  The
+    floor the kernels' times are set against beside the 8 TB/s peak."""
+    from qwen35_amd import abi
+    L = abi.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    pool = torch.empty(pool_mib << 20, dtype=torch.uint8, device="cuda")
+    out = torch.empty(4 * cus, dtype=torch.int32, device="cuda")
+
+    def rd(ptr, n, grid):
+        return lambda: abi.check(L.qh_read_stream(ptr, n, abi.ptr(out), grid, abi.stream_handle()),
+                                 "read_stream")
+
+    def best(launches_for, reps):
+        t = {w: _graph_us(launches_for(w * cus), reps=reps) for w in (1, 2, 3, 4)}
+        w = min(t, key=t.get)
+        return t[w], w
+    rows = []
+    for label, n in READ_FLOOR_SIZES:
+        n16 = (n + 4095) // 4096 * 4096  # slices on 4 KB boundaries
+        k = max(2, pool.numel() // n16)
+        us, wpc = best(lambda grid: [rd(pool.data_ptr() + i * n16, n, grid) for i in range(k)], 10)
+        rows.append({"for": label, "bytes": n, "us": round(us, 3), "GBps": round(n / (us * 1e-6) / 1e9, 1),
+                     "workgroups_per_cu": wpc, "slices": k})
+    lm = eng.w.lm_head
+    n = lm.numel() * lm.element_size()
+    us, wpc = best(lambda grid: [rd(lm.data_ptr(), n, grid)] * 4, 3)
+    rows.append({"for": "lm_head 248320x2560 bf16", "bytes": n, "us": round(us, 3),
+                 "GBps": round(n / (us * 1e-6) / 1e9, 1), "workgroups_per_cu": wpc, "slices": 1})
+    del pool
+    return {"kernel": "read_stream_kernel (qh_read_stream), 256 threads per workgroup",
+            "timing": "HIP graph over the slices, replayed between HIP events; best of 1-4 workgroups per CU",
+            "sizes": rows}
+
+
 def host_cpu():
     """The host's CPU as lscpu reports it (model, sockets, physical cores)."""
     info = {"os_cpu_count": os.cpu_count()}
@@ -699,6 +744,8 @@ def main():
     floor = launch_floor()
     log(f"launch floor: {floor['empty_kernel_us']} us empty kernel, {floor['gemv_128x2560_us']} us "
         f"128x2560 GEMV")
+    rfloor = read_floor(eng)
+    log("read floor: " + ", ".join(f"{r['bytes'] / 1e6:.1f} MB {r['us']} us" for r in rfloor["sizes"]))
     mlp_us, n_launch = time_mlp_launches(eng)
     log(f"gate/up kernel: {mlp_us:.2f} us per launch")
     mbytes = mlp_bytes(cfg)
@@ -708,6 +755,17 @@ def main():
     prefill = time_prefill(eng, prompt.cuda())
     log(f"prefill: {prefill['prompt_tokens']} tokens in {prefill['ms']} ms")
     kernels = kernel_configs(eng, cpu=not args.no_cpu_baseline)
+    # beside each E4M3 / lm_head config: a plain read of its weight bytes in as
+    # many launches (down and config 1 read the same 23.6 MB)
+    fl = {r["for"]: r["us"] for r in rfloor["sizes"]}
+    floors = {"1 GEMV": fl["down 2560x9216"],
+              "2 MLP": fl["gate/up 2 x 9216x2560"] + fl["down 2560x9216"],
+              "3b lm_head": fl["lm_head 248320x2560 bf16"]}
+    for k in kernels:
+        for prefix, f_us in floors.items():
+            if k["config"].startswith(prefix):
+                k["read_floor_us"] = round(f_us, 3)
+                k["frac_of_read_floor"] = round(f_us / k["us"], 4)
     gemm = time_prefill_gemm()
     log("prefill GEMM: " + ", ".join(f"{g['N']}x{g['K']} {g['us']} us ({g['tflops']} TFLOP/s)"
                                      for g in gemm["gemms"]))
@@ -767,10 +825,13 @@ def main():
             "algorithmic_bytes_per_launch": mbytes,
             "mean_launch_us": round(mlp_us, 3),
             "launches_timed": n_launch,
+            "read_floor_us": rfloor["sizes"][4]["us"],
+            "frac_of_read_floor": round(rfloor["sizes"][4]["us"] / mlp_us, 4),
         },
         "cpu_baseline": cpu,
         "memory": mem,
         "launch_floor": floor,
+        "read_floor": rfloor,
         "prefill": prefill,
         "prefill_gemm": gemm,
         "kernels": kernels,

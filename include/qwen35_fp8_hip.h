@@ -220,6 +220,15 @@ int qh_gdn_decode(const void* mixed, const void* a, const void* b, const void* z
                   const int* pos_dev, int pos, int Hk, int Hv, int dk, int dv, float eps,
                   qh_stream_t stream);
 
+/* Measurement helper with no counterpart in the reference: reads `bytes`
+ * bytes at src (16-byte aligned, a non-zero multiple of 16, at most 2^31) in one launch of
+ * min(out_len, 4 x CUs) workgroups with 16-byte loads, each wave streaming a
+ * contiguous share as the GEMVs' waves stream their rows, and writes one XOR
+ * checksum of 32-bit words per workgroup to out.  The XOR of those checksums
+ * is the XOR of all words.  Its time is the plain-read floor that bench.py
+ * sets the decode kernels' times against. */
+int qh_read_stream(const void* src, size_t bytes, unsigned* out, int out_len, qh_stream_t stream);
+
 /* Scratch bytes for qh_lm_head_argmax. */
 size_t qh_lm_head_scratch_bytes(int N);
 

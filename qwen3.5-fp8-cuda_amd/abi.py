@@ -73,6 +73,7 @@ NATIVE_SIGNATURES = {
                            _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "qh_gdn_decode_core": (_i, [_vp] * 10 + [_i] * 5 + [_vp]),
     "qh_gemv_e4m3_gated": (_i, [_vp, _vp, _vp, _i, _f, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "qh_read_stream": (_i, [_vp, _sz, _vp, _i, _vp]),
     "qh_lm_head_scratch_bytes": (_sz, [_i]),
     "qh_lm_head_argmax": (_i, [_vp, _vp, _f, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i,
                                _vp, _vp, _vp, _vp]),

@@ -632,6 +632,13 @@ QH_EXPORT int qh_gemv_e4m3_gated(const void* core, const void* z, const void* no
   return run_gemv(p, scales_bf16 != 0, "qh_gemv_e4m3_gated", stream);
 }
 
+// Plain read of `bytes` bytes (one XOR checksum per workgroup into out, at
+// most out_len workgroups): the measured read floor.
+QH_EXPORT int qh_read_stream(const void* src, size_t bytes, unsigned* out, int out_len, hipStream_t stream) {
+  if (qh_launch_read_stream(src, bytes, out, out_len, stream) != 0) return -1;
+  return check_launch("qh_read_stream");
+}
+
 QH_EXPORT size_t qh_lm_head_scratch_bytes(int N) {
   return (size_t)qh_lm_head_grid(N) * (sizeof(float) + sizeof(int));
 }

@@ -997,6 +997,54 @@ int pick_cpl(int K) {
     default: return -1;                  \
   }
 
+// ---- plain read stream (the measured read floor) ---------------------------
+// Reads `bytes` bytes (< 2^31) with the lm_head's weight load (non-temporal,
+// 16 bytes per lane, so one wave instruction reads 1 KB contiguous).  Wave w of
+// the grid reads its own contiguous `wave_bytes` from byte w * wave_bytes, as
+// the GEMVs' waves stream their rows, in batches of 8 loads with the next batch
+// in flight while one is consumed, and writes one XOR checksum per workgroup so
+// that no load is dead.  Each wave's loads go through a buffer resource over
+// exactly its share: past the end they return zeros without memory traffic,
+// so the loop has no branch and every wave runs the same trip count.  What one
+// launch can read of the same bytes: the floor the decode kernels are measured
+// against beside the 8 TB/s peak.
+__global__ __launch_bounds__(256) void read_stream_kernel(const uint8_t* __restrict__ src, uint32_t bytes,
+                                                          uint32_t wave_bytes, unsigned* __restrict__ out) {
+  constexpr int U = 8;
+  constexpr uint32_t kLoad = 64 * 16;  // bytes per wave load
+  __shared__ unsigned red[4];
+  const int lane = threadIdx.x & 63;
+  const uint32_t w0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * wave_bytes;
+  const uint32_t len = w0 < bytes ? min(wave_bytes, bytes - w0) : 0u;
+  const qh_rsrc r = make_rsrc(src + (w0 < bytes ? w0 : 0u), len);
+  const uint32_t batch = U * kLoad;
+  const uint32_t nb = (wave_bytes + batch - 1) / batch;  // batches, the same in every wave
+  uint32_t off = (uint32_t)lane * 16u;
+  unsigned acc = 0;
+  u32x4 va[U], vb[U];
+  auto issue = [&](u32x4 (&v)[U], uint32_t o) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, o + u * kLoad, 0, 2 /* nt */);
+  };
+  auto consume = [&](const u32x4 (&v)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  };
+  issue(va, off);
+  for (uint32_t b = 0; b < nb; b += 2) {
+    issue(vb, off + batch);
+    consume(va);
+    issue(va, off + 2 * batch);
+    consume(vb);
+    off += 2 * batch;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) acc ^= (unsigned)__shfl_xor((int)acc, m, 64);
+  if (lane == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
 }  // namespace
 
 int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st) {
@@ -1069,6 +1117,22 @@ int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st) {
                      : launch_mlp_t<C, false, float>(p, st)))
   QH_CPL_DISPATCH(cpl, M)
 #undef M
+  return 0;
+}
+
+int qh_launch_read_stream(const void* src, uint64_t bytes, unsigned* out, int out_len, hipStream_t st) {
+  if (!src || !out || out_len < 1 || bytes == 0 || bytes % 16 != 0 || bytes > (1ull << 31) ||
+      ((uintptr_t)src & 15) != 0) {
+    qh_set_error("read_stream: needs a 16-byte aligned source, a non-zero multiple of 16 bytes up to "
+                 "2^31 (got %llu) and an output of at least one word", (unsigned long long)bytes);
+    return -1;
+  }
+  const int grid = std::min(out_len, 4 * cu_count());
+  // each wave's share, whole 1 KB wave loads
+  const uint64_t waves = 4ull * (uint64_t)grid;
+  const uint32_t wave_bytes = (uint32_t)((bytes + waves * 1024 - 1) / (waves * 1024) * 1024);
+  hipLaunchKernelGGL(read_stream_kernel, dim3(grid), dim3(256), 0, st, (const uint8_t*)src, (uint32_t)bytes,
+                     wave_bytes, out);
   return 0;
 }
 

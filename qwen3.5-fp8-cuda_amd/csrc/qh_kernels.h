@@ -80,5 +80,6 @@ int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st);
 int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st);
 int qh_launch_lm_head(QhLmHeadParams p, int grid, hipStream_t st);
 int qh_lm_head_grid(int N);
+int qh_launch_read_stream(const void* src, uint64_t bytes, unsigned* out, int out_len, hipStream_t st);
 
 void qh_set_error(const char* fmt, ...);

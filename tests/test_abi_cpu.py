@@ -101,6 +101,11 @@ def test_validation_errors_need_no_gpu():
     rc = lib.qh_gdn_decode(None, None, None, None, None, None, None, None, None, None, None, None, None,
                            None, 0, 16, 32, 64, 128, 1e-6, None)
     assert rc == -1 and "dk" in abi.last_error()
+    # the plain-read floor: alignment, size and output checks before any launch
+    for src, nbytes, n_out in [(4096, 100, 8), (4100, 4096, 8), (4096, 0, 8), (4096, 4096, 0),
+                               (4096, (1 << 31) + 16, 8)]:
+        rc = lib.qh_read_stream(ctypes.c_void_p(src), nbytes, ctypes.c_void_p(8192), n_out, None)
+        assert rc == -1 and "read_stream" in abi.last_error(), (src, nbytes, n_out)
     # chunked GatedDeltaNet prefill: shape and workspace checks before any launch
     rc = lib.qh_gdn_chunk(None, None, None, None, None, None, None, None, None, 64, 16, 32, 64, 128,
                           1e-6, None, 0, None)

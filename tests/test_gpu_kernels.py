@@ -5,6 +5,7 @@ scales and the native qh_* entry points with fp32 scales.
 """
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -505,6 +506,29 @@ def test_delta_rule_and_gates_reference_abi():
 
 
 # ------------------------------------------------------------------ lm_head
+@pytest.mark.parametrize("nbytes,n_out", [(16, 512), (4096 * 3 + 48, 512), (10 * 2 ** 20 + 16 * 7, 512),
+                                          (2560 * 9216, 512), (2560 * 9216, 3), (2560 * 9216, 256),
+                                          (12352 * 2560, 1024), (12352 * 2560, 4096)])
+def test_read_stream_reads_every_word_once(nbytes, n_out):
+    """qh_read_stream (the measured read floor): the XOR of its per-workgroup
+    checksums equals the XOR of all 32-bit words of the buffer, so every word
+    is read exactly once, whatever the size and grid; workgroups past the grid
+    leave their output words untouched."""
+    g = gen(nbytes % 1000 + n_out)
+    words = torch.randint(-2 ** 31, 2 ** 31, (nbytes // 4,), generator=g, dtype=torch.int64).to(torch.int32)
+    src = words.to(DEV)
+    out = torch.full((n_out + 1,), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+    lib = abi.load()
+    abi.check(lib.qh_read_stream(abi.ptr(src), nbytes, abi.ptr(out), n_out, abi.stream_handle()), "read_stream")
+    sync()
+    got = out.cpu()
+    grid = min(n_out, 4 * torch.cuda.get_device_properties(0).multi_processor_count)
+    expect = int(np.bitwise_xor.reduce(words.numpy().view(np.uint32)))
+    have = int(np.bitwise_xor.reduce(got[:grid].numpy().view(np.uint32)))
+    assert have == expect
+    assert (got[grid:] == 0x5A5A5A5A).all()
+
+
 @pytest.mark.parametrize("V,K", [(1000, 256), (248320, 2560)])
 def test_lm_head_argmax(V, K):
     g = gen(V)
