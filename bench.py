@@ -205,24 +205,50 @@ def time_prefill(eng, prompt, reps=3):
             "timing": f"wall clock, best of {reps}, synchronized before and after"}
 
 
+def _events_us(run, reps):
+    """Mean microseconds of `run` (one launch on the current stream) over
+    `reps` launches after 3 warm-up ones, between HIP events on that stream."""
+    for _ in range(3):
+        run()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(reps):
+        run()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
 def time_prefill_gemm(reps=20):
     """Config-3a GEMMs timed with HIP events on their stream (mean of `reps`
-    launches after warm-up); TFLOP/s = 2*M*N*K / time."""
+    launches after warm-up); TFLOP/s = 2*M*N*K / time.  Beside each: the same
+    GEMM with a split-K workspace (the engine's prefill passes one), and the
+    vendor library's plain bf16 GEMM of the same shape (torch.matmul on the
+    weights dequantized to bf16, i.e. hipBLASLt) as a rate reference: it is
+    not block-scaled E4M3 and not the product path."""
+    from qwen35_amd import abi
+    lib = abi.load()
     res = []
-    for (M, N, K), run in prefill_gemm_launchers(prefill_gemm_inputs()):
-        for _ in range(3):
-            run()
-        st = torch.cuda.current_stream()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(st)
-        for _ in range(reps):
-            run()
-        b.record(st)
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / reps
+    inputs = prefill_gemm_inputs()
+    for ((M, N, K), run), (x, w, s) in zip(prefill_gemm_launchers(inputs), inputs):
+        us = _events_us(run, reps)
         tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        ws = torch.empty(int(lib.qh_gemm_workspace_size(M, K)), dtype=torch.uint8, device="cuda")
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        us_ws = _events_us(lambda: abi.check(lib.qh_gemm_e4m3(
+            abi.ptr(x), abi.ptr(w), abi.ptr(s), abi.ptr(y), M, N, K, K // 128, 0, abi.ptr(ws), ws.numel(),
+            abi.stream_handle()), "gemm ws"), reps)
+        wd = (w.view(torch.float8_e4m3fn).float() *
+              s.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)[:, :K]).to(torch.bfloat16)
+        us_lib = _events_us(lambda: torch.matmul(x, wd.t()), reps)
+        del wd
         res.append({"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
-                    "frac_bf16_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)})
+                    "frac_bf16_dense_peak": round(tf / BF16_MFMA_PEAK_TFLOPS, 4),
+                    "us_with_workspace": round(us_ws, 2),
+                    "hipblaslt_bf16_us": round(us_lib, 2),
+                    "hipblaslt_bf16_frac_dense_peak": round(2.0 * M * N * K / (us_lib * 1e-6) / 1e12
+                                                            / BF16_MFMA_PEAK_TFLOPS, 4)})
     return {"config": "BASELINE configs[2]: X[512x2560] x W[9216x2560]^T and X'[512x9216] x "
                       "W'[2560x9216]^T, E4M3 128x128 block scales, seed 0",
             "kernel": "gemm_dma_kernel (persistent workgroups, 64x64 tiles through a direct-to-LDS "

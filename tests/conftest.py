@@ -27,6 +27,19 @@ def pytest_collection_modifyitems(config, items):
 
 
 @pytest.fixture(scope="session")
+def progress(pytestconfig):
+    """print() that reaches the terminal past pytest's output capture, so a
+    test that runs for minutes shows it is alive to a runner that stops
+    silent jobs."""
+    capman = pytestconfig.pluginmanager.getplugin("capturemanager")
+
+    def say(*args):
+        with capman.global_and_fixture_disabled():
+            print(*args, flush=True)
+    return say
+
+
+@pytest.fixture(scope="session")
 def lib():
     from qwen35_amd import abi
     return abi.load()

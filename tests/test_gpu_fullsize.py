@@ -58,27 +58,28 @@ def _ulp(x):
 
 
 @pytest.fixture(scope="module")
-def model():
+def model(progress):
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     cfg = qwen35_4b()
     w = make_weights(cfg, seed=0, device="cuda")
-    print("config 5 weights drawn; building the oracle", flush=True)
+    progress("\nconfig 5 weights drawn; building the oracle")
     max_seq = N_PROMPT + N_ROWS + 8
     eng = eng_mod.Qwen35FP8Engine(w, max_seq_len=max_seq)
     ref = orc.OracleModel(w.to("cpu"), max_seq_len=max_seq, prefill="reference")
     ref.cos, ref.sin = eng.rope_cos.cpu(), eng.rope_sin.cpu()
+    progress("config 5 oracle built")
     prompt = make_prompt(cfg, n=N_PROMPT, seed=1)
     yield cfg, eng, ref, prompt
     del eng, ref
 
 
 @pytest.mark.timeout(900)
-def test_config5_full_length_within_noise_floor(model):
+def test_config5_full_length_within_noise_floor(model, progress):
     cfg, eng, ref, prompt = model
     g_tr, o_tr = [], []
     gl = eng.prefill_batch(prompt.cuda(), trace=g_tr).float().cpu().view(-1)
     rl = ref.prefill(prompt, trace=o_tr)[0].view(-1)
-    print("prefill per-layer cosine:", [round(cos_sim(a, b), 6) for a, b in zip(g_tr, o_tr)], flush=True)
+    progress("prefill per-layer cosine:", [round(cos_sim(a, b), 6) for a, b in zip(g_tr, o_tr)])
     rows = [(gl, rl)]
     toks, layer_cos = [], {}
     pos = N_PROMPT
@@ -96,7 +97,7 @@ def test_config5_full_length_within_noise_floor(model):
         rows.append((gl.float().cpu().view(-1), rl))
         pos += 1
         if j % 25 == 0:
-            print(f"row {j}/{N_ROWS - 1}: cosine {cos_sim(rows[-1][0], rl):.6f}", flush=True)
+            progress(f"row {j}/{N_ROWS - 1}: cosine {cos_sim(rows[-1][0], rl):.6f}")
     toks.append(orc.argmax_first(rl))
     cos, agree, margin = [], [], []
     for g, r in rows:
