@@ -15,7 +15,10 @@
 //     per wave; E4M3 pairs become bf16 pairs with v_cvt_scalef32_pk_bf16_fp8
 //     and meet the activations in v_dot2_f32_bf16;
 //   * the fp32 scale of the 128-wide K block is applied once per 8-element
-//     partial (an FMA), and partials meet in a 64-lane shuffle reduction.
+//     partial (an FMA), and partials meet in a 64-lane shuffle reduction;
+//   * shapes with at most 48 KB of weights per CU (o_proj / out_proj) instead
+//     put each CU's whole share in flight at once as direct-to-LDS loads
+//     (gemv_lds_kernel), which removes the pipeline's start-up.
 #include "qh_common.h"
 #include "qh_kernels.h"
 
@@ -171,7 +174,27 @@ __device__ __forceinline__ u32x4 gated_bf16x8(u32x4 c, u32x4 z, float rs, u32x4 
 // gd > 0: the per-head gated RMSNorm (heads of gd = 128 elements: a head's 16
 // chunks sit in 16 consecutive threads, an aligned lane group) instead of the
 // x2 sum and the (1+w) RMSNorm.
-template <int CPL, int NT = 256>
+// LDS-only barrier: waits for this wave's LDS writes, not for its vector
+// memory loads (__syncthreads' workgroup fence would also wait for every
+// outstanding load, direct-to-LDS weight loads included).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int NT>
+__device__ __forceinline__ float block_sum_lds(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) red[wid] = v;
+  lds_barrier();
+  float s = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) s += red[w];
+  return s;
+}
+
+// BARE: the barriers wait for LDS only (the caller's loads stay in flight).
+template <int CPL, int NT = 256, bool BARE = false>
 __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, float* red, bool has_x2,
                                                bool has_norm, float eps, int K, int gd = 0) {
   constexpr int MAXC = XIn<CPL, NT>::MAXC;
@@ -198,7 +221,7 @@ __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, f
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
-    ss = block_sum<NT>(ss, red);
+    ss = BARE ? block_sum_lds<NT>(ss, red) : block_sum<NT>(ss, red);
     const float rms = rsqrtf(ss / (float)K + eps);
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) v[i] = norm_bf16x8(v[i], rms, in.w0[i], in.w1[i]);
@@ -208,7 +231,8 @@ __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, f
     const int c = tid + NT * i;
     if (c < nch) *(u32x4*)(sx + c * 8) = v[i];
   }
-  __syncthreads();
+  if (BARE) lds_barrier();
+  else __syncthreads();
 }
 
 // Prologue variant for large K: loads and combines x / x2 in one pass and
@@ -760,6 +784,174 @@ __attribute__((amdgpu_waves_per_eu(2))) void mlp_fast_kernel(QhMlpParams p) {
   mlp_fast_body<CPL, P, ScaleT, NT>(p, blockIdx.x, gridDim.x, sx, red);
 }
 
+// ---- LDS-streamed GEMV: a CU's whole share of the weights in flight ---------
+// For shapes whose rows, split evenly over the CUs, fit in one CU's LDS
+// (160 KB): one 512-thread workgroup per CU owns a contiguous row range, and
+// every wave issues all of its rows at once as 16-byte direct-to-LDS loads
+// (1 KB per wave instruction, no registers held while they fly).  The weight
+// stream then runs like a plain read from the first cycle, and the
+// activation's round trip, the norm and the dot products hide under it.
+// Row slot s of the range belongs to wave s % 8; vector-memory loads
+// complete in order per wave, so a wave waits (vmcnt) for its slot i alone,
+// then reads that row from LDS.  Chunk c of lane l covers bytes
+// [16 (l + 64 c), +16) of the row, i.e. k-block (l + 64 c) / 8.
+typedef __attribute__((address_space(3))) void* qh_lds_ptr;
+constexpr int kLdsThreads = 512;
+constexpr int kLdsWaves = kLdsThreads / 64;
+constexpr uint32_t kLdsBytes = 160u * 1024u;
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 0..63");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Segment of grouped row g and its row index, chosen by scalar selects over
+// the four segments' fields (an indexed p.seg[si] is a kernel-argument load
+// and a wait per row).
+__device__ __forceinline__ QhGemvSeg seg_of(const QhGemvParams& p, int g, int& row) {
+  QhGemvSeg sg = p.seg[0];
+  int g0 = 0;
+#pragma unroll
+  for (int t = 1; t < 4; ++t) {
+    if (t < p.nseg && g >= p.gstart[t]) {
+      sg = p.seg[t];
+      g0 = p.gstart[t];
+    }
+  }
+  row = g - g0;
+  return sg;
+}
+
+// Row slot I of this wave: wait for its loads, dot it against the activation
+// slice, store.  SR: scale registers per row (k-blocks 64 r + l).
+template <int I, int KC, int RPW, int SR>
+__device__ __forceinline__ void lds_rows(const QhGemvParams& p, const uint8_t* rows, int r0, int nrows,
+                                         const u32x4 (&xa)[KC], const u32x4 (&xb)[KC],
+                                         const float (&sc)[RPW][SR], float res, int lane, int wid) {
+  if constexpr (I < RPW) {
+    const int s = wid + kLdsWaves * I;
+    if (s >= nrows) {
+      wait_vmem<0>();  // the remaining slots' (dummy) loads land before the wave ends
+      return;
+    }
+    wait_vmem<(RPW - 1 - I) * KC>();  // the slot's weight loads (the later slots' stay in flight)
+    const uint8_t* base = rows + (size_t)s * KC * 1024;
+    const int K = p.K;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int ch = lane + 64 * c;
+      u32x4 w = *(const u32x4*)(base + c * 1024 + lane * 16);
+      if (16 * ch >= K) w = u32x4{0u, 0u, 0u, 0u};
+      float d = dot8_e4m3_bf16(w.x, w.y, xa[c], 0.0f);
+      d = dot8_e4m3_bf16(w.z, w.w, xb[c], d);
+      // k-block (l + 64 c) / 8 = 8 c + l / 8: lane (8 c + l / 8) % 64 of register c / 8
+      const float scl = __builtin_bit_cast(
+          float, __builtin_amdgcn_ds_bpermute((((lane >> 3) + 8 * c) & 63) * 4,
+                                              __builtin_bit_cast(int, sc[I][c >> 3])));
+      acc = fmaf(d, scl, acc);
+    }
+    const float tot = wave_total(acc);
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + s, row);
+    const float rv = __shfl(res, I, 64);
+    if (lane == 0) {
+      float y = rbf(tot);
+      if (p.res1) y = rv + y;
+      sg.y[out_index(sg, row)] = f2bf(y);
+    }
+    lds_rows<I + 1, KC, RPW, SR>(p, rows, r0, nrows, xa, xb, sc, res, lane, wid);
+  }
+}
+
+// KC: 1 KB chunks per row (ceil(K / 1024)); RPW: row slots per wave.
+template <int KC, int RPW, typename ScaleT>
+__global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
+  constexpr int CPL = 2 * KC;  // 8-element activation chunks per lane (K <= 1024 KC)
+  constexpr int KBMAX = KC * 8;
+  constexpr int SR = (KBMAX + 63) / 64;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int K = p.K;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // contiguous row range of this workgroup (slot s: row r0 + s), sizes
+  // differing by at most one
+  const int G = gridDim.x, b = blockIdx.x;
+  const int base_n = p.gtotal / G, rem = p.gtotal % G;
+  const int nrows = base_n + (b < rem ? 1 : 0);
+  const int r0 = b * base_n + min(b, rem);
+  const int maxrows = base_n + (rem ? 1 : 0);
+  if (nrows == 0) return;
+  uint16_t* sx = (uint16_t*)lds;
+  float* red = (float*)(lds + ((K * 2 + 255) & ~255));
+  uint8_t* rows = lds + ((K * 2 + 255) & ~255) + 256;
+  uint8_t* dummy = rows + (size_t)maxrows * KC * 1024;
+
+  XIn<CPL, kLdsThreads> xin;
+  block_x_load<CPL, kLdsThreads>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
+  // residuals of this wave's row slots: lane i holds slot wid + 8 i
+  // residuals of this wave's row slots (lane i: slot wid + 8 i), raw bf16 bits,
+  // branch-free: one resource over the range, kOob past it or without res
+  uint32_t r1 = 0, r2 = 0;
+  {
+    const int s = wid + kLdsWaves * lane;
+    const uint32_t off = lane < RPW && s < nrows ? (uint32_t)(r0 + s) * 2u : kOob;
+    const uint32_t rb = (uint32_t)p.gtotal * 2u;
+    r1 = bload_u16(make_rsrc(p.res1 ? p.res1 : p.x, p.res1 ? rb : 0u), off);
+    r2 = bload_u16(make_rsrc(p.res2 ? p.res2 : p.x, p.res2 ? rb : 0u), off);
+  }
+  // every slot's scales, then (in this order: completion is in order) every
+  // slot's weight bytes
+  const int KB = K / 128;
+  float sc[RPW][SR];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int s = wid + kLdsWaves * i;
+    const bool valid = s < nrows;
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
+    const qh_rsrc sr = make_rsrc((const ScaleT*)sg.s + (size_t)(row >> 7) * KB,
+                                 valid ? (uint32_t)(KB * sizeof(ScaleT)) : 0u);
+#pragma unroll
+    for (int r = 0; r < SR; ++r) {
+      const uint32_t off = (lane + 64u * r) * (uint32_t)sizeof(ScaleT);
+      if (sizeof(ScaleT) == 4)
+        sc[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
+      else
+        sc[i][r] = bf2f(bload_u16(sr, off));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int s = wid + kLdsWaves * i;
+    const bool valid = s < nrows;
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
+    const qh_rsrc wr = make_rsrc(sg.w + (size_t)row * K, valid ? (uint32_t)K : 0u);
+    uint8_t* dst = valid ? rows + (size_t)s * KC * 1024 : dummy;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (qh_lds_ptr)(dst + c * 1024), 16,
+                                               (uint32_t)(lane * 16 + c * 1024), 0, 0, 2 /* nt */);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  block_x_finish<CPL, kLdsThreads, true>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
+                                         p.gnorm_w ? p.gnorm_d : 0);
+  u32x4 xa[KC], xb[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    const int e = 16 * (lane + 64 * c);
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    xa[c] = e < K ? *(const u32x4*)(sx + e) : zero;
+    xb[c] = e < K ? *(const u32x4*)(sx + e + 8) : zero;
+  }
+  float res = 0.0f;
+  if (p.res1) res = p.res2 ? rbf(bf2f((uint16_t)r1) + bf2f((uint16_t)r2)) : bf2f((uint16_t)r1);
+  lds_rows<0, KC, RPW, SR>(p, rows, r0, nrows, xa, xb, sc, res, lane, wid);
+}
+
 // ---- bf16 lm_head GEMV + greedy argmax -------------------------------------
 // torch.argmax order on the bf16 logits: NaN ranks above every number, and
 // the lowest index wins ties.  Candidates start at (-inf, INT_MAX); the final
@@ -947,6 +1139,62 @@ void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
 
+template <int KC, int RPW, typename ScaleT>
+void launch_gemv_lds_t(const QhGemvParams& p, size_t lds, int G, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_lds_kernel<KC, RPW, ScaleT>), dim3(G), dim3(kLdsThreads), lds, st, p);
+}
+
+// Weight bytes per CU up to which the LDS-streamed GEMV is used.  Measured on
+// MI355X (graph of launches over more weight copies than the MALL holds): a
+// CU streams direct-to-LDS loads at 15-18 GB/s however many waves issue them,
+// below the ~27 GB/s per CU of a plain read, so the whole-share-at-once issue
+// only wins while the share is small enough for the start-up it removes to
+// dominate: 2560 x 4096 (40 KB per CU) 5.01 -> 4.54 us, 4096 x 2560 5.67 ->
+// 4.54 us; at 92-123 KB per CU (down, config 1, qkv, in_proj) it is 0.4-2.4 us
+// slower than the register pipeline.
+constexpr size_t kLdsMaxShare = 48u * 1024u;
+
+// LDS-streamed path when a CU's share of the rows is at most kLdsMaxShare;
+// false when the shape does not qualify (the caller then runs the register
+// pipeline).
+template <typename ScaleT>
+bool try_gemv_lds(const QhGemvParams& p, hipStream_t st) {
+  if (p.K % 512 != 0) return false;
+  const int KC = (p.K + 1023) / 1024;
+  const int G = cu_count();
+  const int maxrows = (p.gtotal + G - 1) / G;
+  const int need = (maxrows + kLdsWaves - 1) / kLdsWaves;
+  const size_t bytes = (size_t)((p.K * 2 + 255) & ~255) + 256 + (size_t)(maxrows + 1) * KC * 1024;
+  if ((size_t)maxrows * p.K > kLdsMaxShare || bytes > kLdsBytes) return false;
+  // more than half the LDS, so no two workgroups share a CU
+  const size_t lds = std::max(bytes, (size_t)kLdsBytes / 2 + 4096);
+#define L(KCV, R) launch_gemv_lds_t<KCV, R, ScaleT>(p, lds, G, st)
+  // wait counts (RPW - 1) KC stay below vmcnt's 64
+  if (need <= 2) {
+    switch (KC) {
+      case 1: L(1, 2); return true;
+      case 2: L(2, 2); return true;
+      case 3: L(3, 2); return true;
+      case 4: L(4, 2); return true;
+      case 5: L(5, 2); return true;
+      case 6: L(6, 2); return true;
+      case 8: L(8, 2); return true;
+      case 9: L(9, 2); return true;
+      default: return false;
+    }
+  }
+  if (need <= 6) {
+    switch (KC) {
+      case 1: L(1, 6); return true;
+      case 2: L(2, 6); return true;
+      case 3: L(3, 6); return true;
+      default: return false;
+    }
+  }
+#undef L
+  return false;
+}
+
 template <int CPL, typename ScaleT>
 void launch_mlp_fast_t(const QhMlpParams& p, hipStream_t st) {
   auto fn = mlp_fast_kernel<CPL, mlp_fast_depth(CPL), ScaleT>;
@@ -1078,6 +1326,7 @@ int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st) {
                  p.gnorm_d);
     return -1;
   }
+  if (fast && (scale_bf16 ? try_gemv_lds<uint16_t>(p, st) : try_gemv_lds<float>(p, st))) return 0;
   if (fast) {
 #define F(C) (scale_bf16 ? launch_gemv_fast_t<C, uint16_t>(p, st) : launch_gemv_fast_t<C, float>(p, st))
     QH_FAST_DISPATCH(p.K / 512, F)

@@ -92,7 +92,9 @@ def test_gemv_fp32_scales(N, K, mode):
     assert_close(y, ref, what=f"gemv {N}x{K} {mode}")
 
 
-@pytest.mark.parametrize("N,K", [(256, 384), (9216, 2560)])
+# 2560 x 4096 and 4096 x 2560 (<= 48 KB of weights per CU) take the
+# LDS-streamed kernel, 9216 x 2560 the register pipeline.
+@pytest.mark.parametrize("N,K", [(256, 384), (9216, 2560), (2560, 4096), (4096, 2560)])
 def test_gemv_reference_abi_bf16_scales(N, K):
     """launch_gemv_v4_extern / v3 with bf16 scale_inv, via the reference-named wrapper."""
     g = gen(3)
@@ -142,9 +144,11 @@ def test_grouped_projections_match_single():
     assert_close(uu, orc.linear(x.float(), orc.dequant(wk, sk.to(torch.bfloat16).float())), what="up")
 
 
-def test_gemv_norm_prologue_and_residual_epilogue():
+# (2560, 2560): the LDS-streamed kernel; the others the register pipeline
+# (one row group in flight for K = 9216, four for K = 2560).
+@pytest.mark.parametrize("N,K", [(2560, 2560), (2560, 9216), (12352, 2560)])
+def test_gemv_norm_prologue_and_residual_epilogue(N, K):
     g = gen(5)
-    K, N = 2560, 2560
     w, s = quant(g, N, K)
     x = bf(randn(g, K))
     nw = randn(g, K, std=0.02)
