@@ -16,9 +16,10 @@
 //     and meet the activations in v_dot2_f32_bf16;
 //   * the fp32 scale of the 128-wide K block is applied once per 8-element
 //     partial (an FMA), and partials meet in a 64-lane shuffle reduction;
-//   * shapes with at most 48 KB of weights per CU (o_proj / out_proj) instead
-//     put each CU's whole share in flight at once as direct-to-LDS loads
-//     (gemv_lds_kernel), which removes the pipeline's start-up.
+//   * shapes whose rows fit in one CU's LDS with at most 5 rows per wave
+//     (down, o_proj / out_proj, qkv, config 1's 9216 x 2560) instead stream
+//     16-byte direct-to-LDS loads, one or two rows per wave in flight
+//     (gemv_lds_kernel).
 #include "qh_common.h"
 #include "qh_kernels.h"
 
@@ -784,17 +785,16 @@ __attribute__((amdgpu_waves_per_eu(2))) void mlp_fast_kernel(QhMlpParams p) {
   mlp_fast_body<CPL, P, ScaleT, NT>(p, blockIdx.x, gridDim.x, sx, red);
 }
 
-// ---- LDS-streamed GEMV: a CU's whole share of the weights in flight ---------
+// ---- LDS-streamed GEMV --------------------------------------------------------
 // For shapes whose rows, split evenly over the CUs, fit in one CU's LDS
-// (160 KB): one 512-thread workgroup per CU owns a contiguous row range, and
-// every wave issues all of its rows at once as 16-byte direct-to-LDS loads
-// (1 KB per wave instruction, no registers held while they fly).  The weight
-// stream then runs like a plain read from the first cycle, and the
-// activation's round trip, the norm and the dot products hide under it.
-// Row slot s of the range belongs to wave s % 8; vector-memory loads
-// complete in order per wave, so a wave waits (vmcnt) for its slot i alone,
-// then reads that row from LDS.  Chunk c of lane l covers bytes
-// [16 (l + 64 c), +16) of the row, i.e. k-block (l + 64 c) / 8.
+// (160 KB): one 512-thread workgroup per CU owns a contiguous row range.  Row
+// slot s of the range belongs to wave s % 8, and each slot has its own LDS
+// slot, so no slot is reused.  Every wave issues its activation, residual and
+// scale loads, then keeps D row slots in flight as 16-byte direct-to-LDS
+// loads (1 KB per wave instruction, no registers held while they fly):
+// vector-memory loads complete in order per wave, so it waits (vmcnt) for
+// slot i alone, issues slot i + D, and reads row i from LDS.  Chunk c of lane
+// l covers bytes [16 (l + 64 c), +16) of the row, i.e. k-block (l + 64 c) / 8.
 typedef __attribute__((address_space(3))) void* qh_lds_ptr;
 constexpr int kLdsThreads = 512;
 constexpr int kLdsWaves = kLdsThreads / 64;
@@ -823,10 +823,26 @@ __device__ __forceinline__ QhGemvSeg seg_of(const QhGemvParams& p, int g, int& r
   return sg;
 }
 
+// Issues row slot s's bytes (KC direct-to-LDS loads; a slot past the range
+// loads nothing into the dummy slot, so every wave issues the same count).
+template <int KC>
+__device__ __forceinline__ void lds_issue(const QhGemvParams& p, uint8_t* rows, uint8_t* dummy, int r0, int nrows,
+                                          int s, int lane) {
+  const bool valid = s < nrows;
+  int row;
+  const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
+  const qh_rsrc wr = make_rsrc(sg.w + (size_t)row * p.K, valid ? (uint32_t)p.K : 0u);
+  uint8_t* dst = valid ? rows + (size_t)s * KC * 1024 : dummy;
+#pragma unroll
+  for (int c = 0; c < KC; ++c)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (qh_lds_ptr)(dst + c * 1024), 16,
+                                             (uint32_t)(lane * 16 + c * 1024), 0, 0, 2 /* nt */);
+}
+
 // Row slot I of this wave: wait for its loads, dot it against the activation
 // slice, store.  SR: scale registers per row (k-blocks 64 r + l).
-template <int I, int KC, int RPW, int SR>
-__device__ __forceinline__ void lds_rows(const QhGemvParams& p, const uint8_t* rows, int r0, int nrows,
+template <int I, int KC, int RPW, int SR, int D>
+__device__ __forceinline__ void lds_rows(const QhGemvParams& p, uint8_t* rows, uint8_t* dummy, int r0, int nrows,
                                          const u32x4 (&xa)[KC], const u32x4 (&xb)[KC],
                                          const float (&sc)[RPW][SR], float res, int lane, int wid) {
   if constexpr (I < RPW) {
@@ -835,7 +851,9 @@ __device__ __forceinline__ void lds_rows(const QhGemvParams& p, const uint8_t* r
       wait_vmem<0>();  // the remaining slots' (dummy) loads land before the wave ends
       return;
     }
-    wait_vmem<(RPW - 1 - I) * KC>();  // the slot's weight loads (the later slots' stay in flight)
+    // the slot's weight loads (the later slots' in flight stay so)
+    wait_vmem<((I + D - 1 < RPW - 1 ? I + D - 1 : RPW - 1) - I) * KC>();
+    if constexpr (I + D < RPW) lds_issue<KC>(p, rows, dummy, r0, nrows, wid + kLdsWaves * (I + D), lane);
     const uint8_t* base = rows + (size_t)s * KC * 1024;
     const int K = p.K;
     float acc = 0.0f;
@@ -861,12 +879,13 @@ __device__ __forceinline__ void lds_rows(const QhGemvParams& p, const uint8_t* r
       if (p.res1) y = rv + y;
       sg.y[out_index(sg, row)] = f2bf(y);
     }
-    lds_rows<I + 1, KC, RPW, SR>(p, rows, r0, nrows, xa, xb, sc, res, lane, wid);
+    lds_rows<I + 1, KC, RPW, SR, D>(p, rows, dummy, r0, nrows, xa, xb, sc, res, lane, wid);
   }
 }
 
-// KC: 1 KB chunks per row (ceil(K / 1024)); RPW: row slots per wave.
-template <int KC, int RPW, typename ScaleT>
+// KC: 1 KB chunks per row (ceil(K / 1024)); RPW: row slots per wave; D: row
+// slots in flight per wave.
+template <int KC, int RPW, typename ScaleT, int D = RPW>
 __global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
   constexpr int CPL = 2 * KC;  // 8-element activation chunks per lane (K <= 1024 KC)
   constexpr int KBMAX = KC * 8;
@@ -924,18 +943,7 @@ __global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int s = wid + kLdsWaves * i;
-    const bool valid = s < nrows;
-    int row;
-    const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
-    const qh_rsrc wr = make_rsrc(sg.w + (size_t)row * K, valid ? (uint32_t)K : 0u);
-    uint8_t* dst = valid ? rows + (size_t)s * KC * 1024 : dummy;
-#pragma unroll
-    for (int c = 0; c < KC; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (qh_lds_ptr)(dst + c * 1024), 16,
-                                               (uint32_t)(lane * 16 + c * 1024), 0, 0, 2 /* nt */);
-  }
+  for (int i = 0; i < D; ++i) lds_issue<KC>(p, rows, dummy, r0, nrows, wid + kLdsWaves * i, lane);
   __builtin_amdgcn_sched_barrier(0);
   block_x_finish<CPL, kLdsThreads, true>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
                                          p.gnorm_w ? p.gnorm_d : 0);
@@ -949,7 +957,7 @@ __global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
   }
   float res = 0.0f;
   if (p.res1) res = p.res2 ? rbf(bf2f((uint16_t)r1) + bf2f((uint16_t)r2)) : bf2f((uint16_t)r1);
-  lds_rows<0, KC, RPW, SR>(p, rows, r0, nrows, xa, xb, sc, res, lane, wid);
+  lds_rows<0, KC, RPW, SR, D>(p, rows, dummy, r0, nrows, xa, xb, sc, res, lane, wid);
 }
 
 // ---- bf16 lm_head GEMV + greedy argmax -------------------------------------
@@ -1139,24 +1147,31 @@ void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
 
+// Row slots in flight per wave: two for rows under 4 KB, one from 4 KB.
+// Measured on MI355X (graph of launches over more weight copies than the
+// MALL holds): putting a CU's whole share in flight at once is slower (a CU
+// then streams direct-to-LDS loads at only 15-18 GB/s, with 8 or 16 waves
+// alike), and pacing the issue restores the rate:
+//   shape        all at once   D = 1     D = 2     D = 3     register pipeline
+//   12352x2560   10.84         9.74      8.46      8.72      8.43
+//   10240x2560    9.40         8.51      7.52      7.86      7.85
+//    9216x2560    8.35         7.74      7.05      7.41      7.08
+//    2560x9216    7.77         6.90      (all)               7.35
+//    2560x4096    4.55         4.28      (all)               5.01
+constexpr int lds_depth(int kc) { return kc >= 4 ? 1 : 2; }
+
 template <int KC, int RPW, typename ScaleT>
 void launch_gemv_lds_t(const QhGemvParams& p, size_t lds, int G, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_lds_kernel<KC, RPW, ScaleT>), dim3(G), dim3(kLdsThreads), lds, st, p);
+  constexpr int D = lds_depth(KC) < RPW ? lds_depth(KC) : RPW;
+  hipLaunchKernelGGL((gemv_lds_kernel<KC, RPW, ScaleT, D>), dim3(G), dim3(kLdsThreads), lds, st, p);
 }
 
-// Weight bytes per CU up to which the LDS-streamed GEMV is used.  Measured on
-// MI355X (graph of launches over more weight copies than the MALL holds): a
-// CU streams direct-to-LDS loads at 15-18 GB/s however many waves issue them,
-// below the ~27 GB/s per CU of a plain read, so the whole-share-at-once issue
-// only wins while the share is small enough for the start-up it removes to
-// dominate: 2560 x 4096 (40 KB per CU) 5.01 -> 4.54 us, 4096 x 2560 5.67 ->
-// 4.54 us; at 92-123 KB per CU (down, config 1, qkv, in_proj) it is 0.4-2.4 us
-// slower than the register pipeline.
-constexpr size_t kLdsMaxShare = 48u * 1024u;
-
-// LDS-streamed path when a CU's share of the rows is at most kLdsMaxShare;
-// false when the shape does not qualify (the caller then runs the register
-// pipeline).
+// LDS-streamed path when a CU's share of the rows fits in its LDS with at
+// most 5 row slots per wave; false when the shape does not qualify (the
+// caller then runs the register pipeline).  The GatedDeltaNet in_proj
+// (12352 x 2560: 49 rows per CU, 7 slots, 158 KB of LDS) ties with the
+// register pipeline alone and lost in the decode step (728 against 734 tok/s),
+// so it keeps the register pipeline.
 template <typename ScaleT>
 bool try_gemv_lds(const QhGemvParams& p, hipStream_t st) {
   if (p.K % 512 != 0) return false;
@@ -1165,11 +1180,12 @@ bool try_gemv_lds(const QhGemvParams& p, hipStream_t st) {
   const int maxrows = (p.gtotal + G - 1) / G;
   const int need = (maxrows + kLdsWaves - 1) / kLdsWaves;
   const size_t bytes = (size_t)((p.K * 2 + 255) & ~255) + 256 + (size_t)(maxrows + 1) * KC * 1024;
-  if ((size_t)maxrows * p.K > kLdsMaxShare || bytes > kLdsBytes) return false;
+  if (bytes > kLdsBytes) return false;
   // more than half the LDS, so no two workgroups share a CU
   const size_t lds = std::max(bytes, (size_t)kLdsBytes / 2 + 4096);
 #define L(KCV, R) launch_gemv_lds_t<KCV, R, ScaleT>(p, lds, G, st)
-  // wait counts (RPW - 1) KC stay below vmcnt's 64
+  // LDS bounds the rows per CU (160 KB: 2.5 KB rows x 62, 4 KB rows x 38,
+  // 9 KB rows x 16), and the wait counts (D - 1) KC stay below vmcnt's 64
   if (need <= 2) {
     switch (KC) {
       case 1: L(1, 2); return true;
@@ -1183,11 +1199,12 @@ bool try_gemv_lds(const QhGemvParams& p, hipStream_t st) {
       default: return false;
     }
   }
-  if (need <= 6) {
+  if (need <= 5) {
     switch (KC) {
-      case 1: L(1, 6); return true;
-      case 2: L(2, 6); return true;
-      case 3: L(3, 6); return true;
+      case 1: L(1, 5); return true;
+      case 2: L(2, 5); return true;
+      case 3: L(3, 5); return true;
+      case 4: L(4, 5); return true;
       default: return false;
     }
   }
