@@ -16,10 +16,9 @@
 //     and meet the activations in v_dot2_f32_bf16;
 //   * the fp32 scale of the 128-wide K block is applied once per 8-element
 //     partial (an FMA), and partials meet in a 64-lane shuffle reduction;
-//   * shapes whose rows fit in one CU's LDS with at most 5 rows per wave
-//     (down, o_proj / out_proj, qkv, config 1's 9216 x 2560) instead stream
-//     16-byte direct-to-LDS loads, one or two rows per wave in flight
-//     (gemv_lds_kernel).
+//   * the decode path runs the 128-bit paced kernels instead
+//     (gemv_b128_kernel, mlp_b128_kernel): one workgroup per CU over a
+//     contiguous row range, 16-byte loads, one or two rows per wave in flight.
 #include "qh_common.h"
 #include "qh_kernels.h"
 
@@ -175,15 +174,15 @@ __device__ __forceinline__ u32x4 gated_bf16x8(u32x4 c, u32x4 z, float rs, u32x4 
 // gd > 0: the per-head gated RMSNorm (heads of gd = 128 elements: a head's 16
 // chunks sit in 16 consecutive threads, an aligned lane group) instead of the
 // x2 sum and the (1+w) RMSNorm.
-// LDS-only barrier: waits for this wave's LDS writes, not for its vector
-// memory loads (__syncthreads' workgroup fence would also wait for every
-// outstanding load, direct-to-LDS weight loads included).
+// Bare barrier: waits for this wave's LDS writes, not for its vector-memory
+// loads (__syncthreads' workgroup fence would also wait for every weight
+// load in flight).
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <int NT>
-__device__ __forceinline__ float block_sum_lds(float v, float* red) {
+__device__ __forceinline__ float block_sum_bare(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) red[wid] = v;
@@ -222,7 +221,7 @@ __device__ __forceinline__ void block_x_finish(XIn<CPL, NT>& in, uint16_t* sx, f
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) ss = sumsq_bf16x8(v[i], ss);
-    ss = BARE ? block_sum_lds<NT>(ss, red) : block_sum<NT>(ss, red);
+    ss = BARE ? block_sum_bare<NT>(ss, red) : block_sum<NT>(ss, red);
     const float rms = rsqrtf(ss / (float)K + eps);
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) v[i] = norm_bf16x8(v[i], rms, in.w0[i], in.w1[i]);
@@ -785,26 +784,22 @@ __attribute__((amdgpu_waves_per_eu(2))) void mlp_fast_kernel(QhMlpParams p) {
   mlp_fast_body<CPL, P, ScaleT, NT>(p, blockIdx.x, gridDim.x, sx, red);
 }
 
-// ---- LDS-streamed GEMV --------------------------------------------------------
-// For shapes whose rows, split evenly over the CUs, fit in one CU's LDS
-// (160 KB): one 512-thread workgroup per CU owns a contiguous row range.  Row
-// slot s of the range belongs to wave s % 8, and each slot has its own LDS
-// slot, so no slot is reused.  Every wave issues its activation, residual and
-// scale loads, then keeps D row slots in flight as 16-byte direct-to-LDS
-// loads (1 KB per wave instruction, no registers held while they fly):
-// vector-memory loads complete in order per wave, so it waits (vmcnt) for
-// slot i alone, issues slot i + D, and reads row i from LDS.  Chunk c of lane
-// l covers bytes [16 (l + 64 c), +16) of the row, i.e. k-block (l + 64 c) / 8.
-typedef __attribute__((address_space(3))) void* qh_lds_ptr;
-constexpr int kLdsThreads = 512;
-constexpr int kLdsWaves = kLdsThreads / 64;
-constexpr uint32_t kLdsBytes = 160u * 1024u;
+// ---- 128-bit paced GEMV (a CU's contiguous row range) ------------------------
+// One 512-thread workgroup per CU owns a contiguous range of rows (row slots
+// s = 0 .. nrows - 1; slot s belongs to wave s % 8).  Each wave issues its
+// activation and residual loads, then keeps D row slots in flight: a slot is
+// the row's bytes as 16-byte loads (chunk c of lane l covers bytes
+// [16 (l + 64 c), +16), so one wave instruction reads 1 KB contiguous) and
+// its k-block scales, in registers.  After a slot's dot product the wave
+// issues the slot D further on into the same registers.  Every CU's share
+// streams from its first cycle at about 5 KB in flight per wave (D = 2 for
+// 2.5 KB rows, D = 1 from 4 KB): deeper pacing, the whole share at once, and
+// direct-to-LDS loads all measured slower.
+constexpr int kB128Threads = 512;
+constexpr int kB128Waves = kB128Threads / 64;
 
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-  static_assert(N >= 0 && N < 64, "vmcnt holds 0..63");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
+// Row slots in flight per wave for KC 1 KB chunks per row.
+constexpr int b128_depth(int kc) { return kc >= 4 ? 1 : 2; }
 
 // Segment of grouped row g and its row index, chosen by scalar selects over
 // the four segments' fields (an indexed p.seg[si] is a kernel-argument load
@@ -823,131 +818,42 @@ __device__ __forceinline__ QhGemvSeg seg_of(const QhGemvParams& p, int g, int& r
   return sg;
 }
 
-// Issues row slot s's bytes (KC direct-to-LDS loads; a slot past the range
-// loads nothing into the dummy slot, so every wave issues the same count).
+// Scale registers of a row with KC 1 KB chunks: lane l holds k-block
+// 64 r + l of the row's 128-row block.
 template <int KC>
-__device__ __forceinline__ void lds_issue(const QhGemvParams& p, uint8_t* rows, uint8_t* dummy, int r0, int nrows,
-                                          int s, int lane) {
-  const bool valid = s < nrows;
-  int row;
-  const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
-  const qh_rsrc wr = make_rsrc(sg.w + (size_t)row * p.K, valid ? (uint32_t)p.K : 0u);
-  uint8_t* dst = valid ? rows + (size_t)s * KC * 1024 : dummy;
-#pragma unroll
-  for (int c = 0; c < KC; ++c)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (qh_lds_ptr)(dst + c * 1024), 16,
-                                             (uint32_t)(lane * 16 + c * 1024), 0, 0, 2 /* nt */);
-}
+constexpr int b128_sregs() { return (KC * 8 + 63) / 64; }
 
-// Row slot I of this wave: wait for its loads, dot it against the activation
-// slice, store.  SR: scale registers per row (k-blocks 64 r + l).
-template <int I, int KC, int RPW, int SR, int D>
-__device__ __forceinline__ void lds_rows(const QhGemvParams& p, uint8_t* rows, uint8_t* dummy, int r0, int nrows,
-                                         const u32x4 (&xa)[KC], const u32x4 (&xb)[KC],
-                                         const float (&sc)[RPW][SR], float res, int lane, int wid) {
-  if constexpr (I < RPW) {
-    const int s = wid + kLdsWaves * I;
-    if (s >= nrows) {
-      wait_vmem<0>();  // the remaining slots' (dummy) loads land before the wave ends
-      return;
-    }
-    // the slot's weight loads (the later slots' in flight stay so)
-    wait_vmem<((I + D - 1 < RPW - 1 ? I + D - 1 : RPW - 1) - I) * KC>();
-    if constexpr (I + D < RPW) lds_issue<KC>(p, rows, dummy, r0, nrows, wid + kLdsWaves * (I + D), lane);
-    const uint8_t* base = rows + (size_t)s * KC * 1024;
-    const int K = p.K;
-    float acc = 0.0f;
+// Lane partial of one row: chunk c holds k-block (l + 64 c) / 8 = 8 c + l / 8,
+// i.e. lane (8 c + l / 8) % 64 of scale register c / 8 (fetched with
+// ds_bpermute); chunks past K count zero.
+template <int KC>
+__device__ __forceinline__ float b128_dot(const u32x4 (&w)[KC], const float (&sc)[b128_sregs<KC>()],
+                                          const u32x4 (&xa)[KC], const u32x4 (&xb)[KC], int K, int lane) {
+  float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const int ch = lane + 64 * c;
-      u32x4 w = *(const u32x4*)(base + c * 1024 + lane * 16);
-      if (16 * ch >= K) w = u32x4{0u, 0u, 0u, 0u};
-      float d = dot8_e4m3_bf16(w.x, w.y, xa[c], 0.0f);
-      d = dot8_e4m3_bf16(w.z, w.w, xb[c], d);
-      // k-block (l + 64 c) / 8 = 8 c + l / 8: lane (8 c + l / 8) % 64 of register c / 8
-      const float scl = __builtin_bit_cast(
-          float, __builtin_amdgcn_ds_bpermute((((lane >> 3) + 8 * c) & 63) * 4,
-                                              __builtin_bit_cast(int, sc[I][c >> 3])));
-      acc = fmaf(d, scl, acc);
-    }
-    const float tot = wave_total(acc);
-    int row;
-    const QhGemvSeg sg = seg_of(p, r0 + s, row);
-    const float rv = __shfl(res, I, 64);
-    if (lane == 0) {
-      float y = rbf(tot);
-      if (p.res1) y = rv + y;
-      sg.y[out_index(sg, row)] = f2bf(y);
-    }
-    lds_rows<I + 1, KC, RPW, SR, D>(p, rows, dummy, r0, nrows, xa, xb, sc, res, lane, wid);
+  for (int c = 0; c < KC; ++c) {
+    u32x4 ww = w[c];
+    if (16 * (lane + 64 * c) >= K) ww = u32x4{0u, 0u, 0u, 0u};
+    float d = dot8_e4m3_bf16(ww.x, ww.y, xa[c], 0.0f);
+    d = dot8_e4m3_bf16(ww.z, ww.w, xb[c], d);
+    const float scl = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((((lane >> 3) + 8 * c) & 63) * 4, __builtin_bit_cast(int, sc[c >> 3])));
+    acc = fmaf(d, scl, acc);
   }
+  return acc;
 }
 
-// KC: 1 KB chunks per row (ceil(K / 1024)); RPW: row slots per wave; D: row
-// slots in flight per wave.
-template <int KC, int RPW, typename ScaleT, int D = RPW>
-__global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
-  constexpr int CPL = 2 * KC;  // 8-element activation chunks per lane (K <= 1024 KC)
-  constexpr int KBMAX = KC * 8;
-  constexpr int SR = (KBMAX + 63) / 64;
-  extern __shared__ __align__(16) uint8_t lds[];
-  const int K = p.K;
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // contiguous row range of this workgroup (slot s: row r0 + s), sizes
-  // differing by at most one
+// This workgroup's contiguous range of n items (sizes differing by at most one).
+__device__ __forceinline__ void b128_range(int n, int& r0, int& nrows) {
   const int G = gridDim.x, b = blockIdx.x;
-  const int base_n = p.gtotal / G, rem = p.gtotal % G;
-  const int nrows = base_n + (b < rem ? 1 : 0);
-  const int r0 = b * base_n + min(b, rem);
-  const int maxrows = base_n + (rem ? 1 : 0);
-  if (nrows == 0) return;
-  uint16_t* sx = (uint16_t*)lds;
-  float* red = (float*)(lds + ((K * 2 + 255) & ~255));
-  uint8_t* rows = lds + ((K * 2 + 255) & ~255) + 256;
-  uint8_t* dummy = rows + (size_t)maxrows * KC * 1024;
+  const int base = n / G, rem = n % G;
+  nrows = base + (b < rem ? 1 : 0);
+  r0 = b * base + min(b, rem);
+}
 
-  XIn<CPL, kLdsThreads> xin;
-  block_x_load<CPL, kLdsThreads>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
-  // residuals of this wave's row slots: lane i holds slot wid + 8 i
-  // residuals of this wave's row slots (lane i: slot wid + 8 i), raw bf16 bits,
-  // branch-free: one resource over the range, kOob past it or without res
-  uint32_t r1 = 0, r2 = 0;
-  {
-    const int s = wid + kLdsWaves * lane;
-    const uint32_t off = lane < RPW && s < nrows ? (uint32_t)(r0 + s) * 2u : kOob;
-    const uint32_t rb = (uint32_t)p.gtotal * 2u;
-    r1 = bload_u16(make_rsrc(p.res1 ? p.res1 : p.x, p.res1 ? rb : 0u), off);
-    r2 = bload_u16(make_rsrc(p.res2 ? p.res2 : p.x, p.res2 ? rb : 0u), off);
-  }
-  // every slot's scales, then (in this order: completion is in order) every
-  // slot's weight bytes
-  const int KB = K / 128;
-  float sc[RPW][SR];
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int s = wid + kLdsWaves * i;
-    const bool valid = s < nrows;
-    int row;
-    const QhGemvSeg sg = seg_of(p, r0 + (valid ? s : 0), row);
-    const qh_rsrc sr = make_rsrc((const ScaleT*)sg.s + (size_t)(row >> 7) * KB,
-                                 valid ? (uint32_t)(KB * sizeof(ScaleT)) : 0u);
-#pragma unroll
-    for (int r = 0; r < SR; ++r) {
-      const uint32_t off = (lane + 64u * r) * (uint32_t)sizeof(ScaleT);
-      if (sizeof(ScaleT) == 4)
-        sc[i][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
-      else
-        sc[i][r] = bf2f(bload_u16(sr, off));
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < D; ++i) lds_issue<KC>(p, rows, dummy, r0, nrows, wid + kLdsWaves * i, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  block_x_finish<CPL, kLdsThreads, true>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
-                                         p.gnorm_w ? p.gnorm_d : 0);
-  u32x4 xa[KC], xb[KC];
+// The activation slice of the 16-byte chunk layout, from the staged LDS copy.
+template <int KC>
+__device__ __forceinline__ void b128_x(u32x4 (&xa)[KC], u32x4 (&xb)[KC], const uint16_t* sx, int K, int lane) {
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     const int e = 16 * (lane + 64 * c);
@@ -955,9 +861,186 @@ __global__ __launch_bounds__(kLdsThreads) void gemv_lds_kernel(QhGemvParams p) {
     xa[c] = e < K ? *(const u32x4*)(sx + e) : zero;
     xb[c] = e < K ? *(const u32x4*)(sx + e + 8) : zero;
   }
+}
+
+// Scales of a row (no weights): lane l loads k-block 64 r + l of the row's
+// 128-row block.
+template <int KC, typename ScaleT>
+__device__ __forceinline__ void b128_scales(float (&sc)[b128_sregs<KC>()], const void* S, int row, bool valid,
+                                            int K, int lane) {
+  const int KB = K / 128;
+  const qh_rsrc sr = make_rsrc((const ScaleT*)S + (size_t)(row >> 7) * KB, valid ? (uint32_t)(KB * sizeof(ScaleT)) : 0u);
+#pragma unroll
+  for (int r = 0; r < b128_sregs<KC>(); ++r) {
+    const uint32_t off = (lane + 64u * r) * (uint32_t)sizeof(ScaleT);
+    if (sizeof(ScaleT) == 4)
+      sc[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0));
+    else
+      sc[r] = bf2f(bload_u16(sr, off));
+  }
+}
+
+// One row's bytes as 16-byte loads (rows past the range load nothing).
+template <int KC>
+__device__ __forceinline__ void b128_row(u32x4 (&w)[KC], const uint8_t* W, int row, bool valid, int K, int lane) {
+  const qh_rsrc wr = make_rsrc(W + (size_t)row * K, valid ? (uint32_t)K : 0u);
+#pragma unroll
+  for (int c = 0; c < KC; ++c)
+    w[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, (uint32_t)(lane * 16 + c * 1024), 0,
+                                                                          2 /* nt: streaming */));
+}
+
+// Slot I of this wave (row r0 + wid + 8 I): dot product from register set
+// I % D, then slot I + D into the same set.  Unrolled at compile time, so
+// every register index is static and the compiler's in-order vmcnt count
+// waits for slot I's loads only.
+template <int I, int KC, int RPW, int D>
+__device__ __forceinline__ void b128_rows(const QhGemvParams& p, u32x4 (&w)[D][KC],
+                                          const float (&sc)[RPW][b128_sregs<KC>()], const u32x4 (&xa)[KC],
+                                          const u32x4 (&xb)[KC], float res, int r0, int mine, int lane, int wid) {
+  if constexpr (I < RPW) {
+    if (I >= mine) return;
+    const int K = p.K;
+    const float part = b128_dot<KC>(w[I % D], sc[I], xa, xb, K, lane);
+    if constexpr (I + D < RPW) {
+      const bool valid = I + D < mine;
+      int row;
+      const QhGemvSeg sn = seg_of(p, r0 + (valid ? wid + kB128Waves * (I + D) : 0), row);
+      b128_row<KC>(w[I % D], sn.w, row, valid, K, lane);
+    }
+    const float tot = wave_total(part);
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + wid + kB128Waves * I, row);
+    const float rv = __shfl(res, I, 64);
+    if (lane == 0) {
+      float y = rbf(tot);
+      if (p.res1) y = rv + y;
+      sg.y[out_index(sg, row)] = f2bf(y);
+    }
+    b128_rows<I + 1, KC, RPW, D>(p, w, sc, xa, xb, res, r0, mine, lane, wid);
+  }
+}
+
+// KC: 1 KB chunks per row; RPW: row slots per wave (at least the launch's).
+template <int KC, int RPW, typename ScaleT>
+__global__ __launch_bounds__(kB128Threads) void gemv_b128_kernel(QhGemvParams p) {
+  constexpr int D = b128_depth(KC) < RPW ? b128_depth(KC) : RPW;
+  constexpr int SR = b128_sregs<KC>();
+  constexpr int W8 = kB128Waves;
+  __shared__ __align__(16) uint16_t sx[KC * 1024];
+  __shared__ float red[W8];
+  const int K = p.K;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int r0, nrows;
+  b128_range(p.gtotal, r0, nrows);
+  if (nrows == 0) return;
+  const int mine = (nrows - wid + W8 - 1) / W8;  // this wave's slots (<= RPW, checked on the host)
+
+  // in this order (loads complete in order): activation, residuals, every
+  // slot's scales, the first D slots' rows
+  XIn<2 * KC, kB128Threads> xin;
+  block_x_load<2 * KC, kB128Threads>(xin, p.x, p.x2, p.norm_w, K, p.gnorm_w, p.gnorm_d);
+  // residuals of this wave's slots (lane i: slot wid + 8 i) as raw bf16 bits,
+  // branch-free: one resource over the range, kOob past it or without res
+  uint32_t r1, r2;
+  {
+    const uint32_t off = lane < mine ? (uint32_t)(r0 + wid + W8 * lane) * 2u : kOob;
+    const uint32_t rb = (uint32_t)p.gtotal * 2u;
+    r1 = bload_u16(make_rsrc(p.res1 ? p.res1 : p.x, p.res1 ? rb : 0u), off);
+    r2 = bload_u16(make_rsrc(p.res2 ? p.res2 : p.x, p.res2 ? rb : 0u), off);
+  }
+  float sc[RPW][SR];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const bool valid = i < mine;
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + (valid ? wid + W8 * i : 0), row);
+    b128_scales<KC, ScaleT>(sc[i], sg.s, row, valid, K, lane);
+  }
+  u32x4 w[D][KC];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const bool valid = i < mine;
+    int row;
+    const QhGemvSeg sg = seg_of(p, r0 + (valid ? wid + W8 * i : 0), row);
+    b128_row<KC>(w[i], sg.w, row, valid, K, lane);
+  }
+  block_x_finish<2 * KC, kB128Threads, true>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K,
+                                             p.gnorm_w ? p.gnorm_d : 0);
+  u32x4 xa[KC], xb[KC];
+  b128_x<KC>(xa, xb, sx, K, lane);
   float res = 0.0f;
   if (p.res1) res = p.res2 ? rbf(bf2f((uint16_t)r1) + bf2f((uint16_t)r2)) : bf2f((uint16_t)r1);
-  lds_rows<0, KC, RPW, SR, D>(p, rows, dummy, r0, nrows, xa, xb, sc, res, lane, wid);
+  b128_rows<0, KC, RPW, D>(p, w, sc, xa, xb, res, r0, mine, lane, wid);
+}
+
+// Paired gate/up with the SiLU(g) * u epilogue: a slot is gate row r and up
+// row r (5 KB at K = 2560; one slot in flight per wave).
+template <int I, int KC, int RPW>
+__device__ __forceinline__ void b128_pairs(const QhMlpParams& p, u32x4 (&wg)[KC], u32x4 (&wu)[KC],
+                                           const float (&sg)[RPW][b128_sregs<KC>()],
+                                           const float (&su)[RPW][b128_sregs<KC>()], const u32x4 (&xa)[KC],
+                                           const u32x4 (&xb)[KC], int r0, int mine, int lane, int wid) {
+  if constexpr (I < RPW) {
+    if (I >= mine) return;
+    const int K = p.K;
+    const float pg = b128_dot<KC>(wg, sg[I], xa, xb, K, lane);
+    const float pu = b128_dot<KC>(wu, su[I], xa, xb, K, lane);
+    if constexpr (I + 1 < RPW) {
+      const bool valid = I + 1 < mine;
+      const int row = r0 + (valid ? wid + kB128Waves * (I + 1) : 0);
+      b128_row<KC>(wg, p.wg, row, valid, K, lane);
+      b128_row<KC>(wu, p.wu, row, valid, K, lane);
+    }
+    const float ag = wave_total(pg);
+    const float au = wave_total(pu);
+    if (lane == 0) {
+      const int g = r0 + wid + kB128Waves * I;
+      // SiLU on the fp32 accumulators (fused_kernels.cu:476).
+      p.m_out[g] = f2bf(qh_silu(ag) * au);
+      if (p.g_out) p.g_out[g] = f2bf(ag);
+      if (p.u_out) p.u_out[g] = f2bf(au);
+    }
+    b128_pairs<I + 1, KC, RPW>(p, wg, wu, sg, su, xa, xb, r0, mine, lane, wid);
+  }
+}
+
+template <int KC, int RPW, typename ScaleT>
+__global__ __launch_bounds__(kB128Threads) void mlp_b128_kernel(QhMlpParams p) {
+  constexpr int SR = b128_sregs<KC>();
+  constexpr int W8 = kB128Waves;
+  __shared__ __align__(16) uint16_t sx[KC * 1024];
+  __shared__ float red[W8];
+  const int K = p.K;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int r0, nrows;
+  b128_range(p.N, r0, nrows);
+  if (nrows == 0) return;
+  const int mine = (nrows - wid + W8 - 1) / W8;
+
+  XIn<2 * KC, kB128Threads> xin;
+  block_x_load<2 * KC, kB128Threads>(xin, p.x, p.x2, p.norm_w, K);
+  float sg[RPW][SR], su[RPW][SR];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const bool valid = i < mine;
+    const int row = r0 + (valid ? wid + W8 * i : 0);
+    b128_scales<KC, ScaleT>(sg[i], p.sg, row, valid, K, lane);
+    b128_scales<KC, ScaleT>(su[i], p.su, row, valid, K, lane);
+  }
+  u32x4 wg[KC], wu[KC];
+  {
+    const bool valid = 0 < mine;
+    const int row = r0 + wid;
+    b128_row<KC>(wg, p.wg, row, valid, K, lane);
+    b128_row<KC>(wu, p.wu, row, valid, K, lane);
+  }
+  block_x_finish<2 * KC, kB128Threads, true>(xin, sx, red, p.x2 != nullptr, p.norm_w != nullptr, p.eps, K);
+  u32x4 xa[KC], xb[KC];
+  b128_x<KC>(xa, xb, sx, K, lane);
+  b128_pairs<0, KC, RPW>(p, wg, wu, sg, su, xa, xb, r0, mine, lane, wid);
 }
 
 // ---- bf16 lm_head GEMV + greedy argmax -------------------------------------
@@ -1147,69 +1230,72 @@ void launch_gemv_fast_t(const QhGemvParams& p, hipStream_t st) {
   hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, st, p);
 }
 
-// Row slots in flight per wave: two for rows under 4 KB, one from 4 KB.
-// Measured on MI355X (graph of launches over more weight copies than the
-// MALL holds): putting a CU's whole share in flight at once is slower (a CU
-// then streams direct-to-LDS loads at only 15-18 GB/s, with 8 or 16 waves
-// alike), and pacing the issue restores the rate:
-//   shape        all at once   D = 1     D = 2     D = 3     register pipeline
-//   12352x2560   10.84         9.74      8.46      8.72      8.43
-//   10240x2560    9.40         8.51      7.52      7.86      7.85
-//    9216x2560    8.35         7.74      7.05      7.41      7.08
-//    2560x9216    7.77         6.90      (all)               7.35
-//    2560x4096    4.55         4.28      (all)               5.01
-constexpr int lds_depth(int kc) { return kc >= 4 ? 1 : 2; }
-
-template <int KC, int RPW, typename ScaleT>
-void launch_gemv_lds_t(const QhGemvParams& p, size_t lds, int G, hipStream_t st) {
-  constexpr int D = lds_depth(KC) < RPW ? lds_depth(KC) : RPW;
-  hipLaunchKernelGGL((gemv_lds_kernel<KC, RPW, ScaleT, D>), dim3(G), dim3(kLdsThreads), lds, st, p);
+// 128-bit paced kernels: every shape whose rows split over the CUs leave at
+// most 64 slots per wave (K = 1024 KC for the instantiated KC, K % 512 == 0).
+// Measured on MI355X against the register pipeline (gemv_fast_kernel /
+// mlp_fast_kernel), graphs over more weight copies than the MALL holds:
+//   12352 x 2560  8.43 -> 7.92 us    10240 x 2560  7.85 -> 6.81 us
+//    9216 x 2560  7.08 -> 6.43 us     2560 x 9216  7.35 -> 6.47 us
+//    2560 x 4096  5.01 -> 4.06 us     gate/up 2 x 9216 x 2560  9.48 -> 9.32 us
+// Row slots per wave instantiated: 2, 5 or 7 (the launch's count rounded up).
+inline int b128_rpw(int n) {
+  const int need = (n + cu_count() - 1) / cu_count();
+  const int per_wave = (need + kB128Waves - 1) / kB128Waves;
+  return per_wave <= 2 ? 2 : per_wave <= 5 ? 5 : per_wave <= 7 ? 7 : 0;
 }
 
-// LDS-streamed path when a CU's share of the rows fits in its LDS with at
-// most 5 row slots per wave; false when the shape does not qualify (the
-// caller then runs the register pipeline).  The GatedDeltaNet in_proj
-// (12352 x 2560: 49 rows per CU, 7 slots, 158 KB of LDS) ties with the
-// register pipeline alone and lost in the decode step (728 against 734 tok/s),
-// so it keeps the register pipeline.
 template <typename ScaleT>
-bool try_gemv_lds(const QhGemvParams& p, hipStream_t st) {
+bool try_gemv_b128(const QhGemvParams& p, hipStream_t st) {
   if (p.K % 512 != 0) return false;
-  const int KC = (p.K + 1023) / 1024;
-  const int G = cu_count();
-  const int maxrows = (p.gtotal + G - 1) / G;
-  const int need = (maxrows + kLdsWaves - 1) / kLdsWaves;
-  const size_t bytes = (size_t)((p.K * 2 + 255) & ~255) + 256 + (size_t)(maxrows + 1) * KC * 1024;
-  if (bytes > kLdsBytes) return false;
-  // more than half the LDS, so no two workgroups share a CU
-  const size_t lds = std::max(bytes, (size_t)kLdsBytes / 2 + 4096);
-#define L(KCV, R) launch_gemv_lds_t<KCV, R, ScaleT>(p, lds, G, st)
-  // LDS bounds the rows per CU (160 KB: 2.5 KB rows x 62, 4 KB rows x 38,
-  // 9 KB rows x 16), and the wait counts (D - 1) KC stay below vmcnt's 64
-  if (need <= 2) {
-    switch (KC) {
-      case 1: L(1, 2); return true;
-      case 2: L(2, 2); return true;
-      case 3: L(3, 2); return true;
-      case 4: L(4, 2); return true;
-      case 5: L(5, 2); return true;
-      case 6: L(6, 2); return true;
-      case 8: L(8, 2); return true;
-      case 9: L(9, 2); return true;
-      default: return false;
-    }
+  const int rpw = b128_rpw(p.gtotal);
+  const dim3 grid(cu_count()), block(kB128Threads);
+#define B(KCV)                                                                                     \
+  do {                                                                                             \
+    if (rpw == 2) hipLaunchKernelGGL((gemv_b128_kernel<KCV, 2, ScaleT>), grid, block, 0, st, p);   \
+    else if (rpw == 5) hipLaunchKernelGGL((gemv_b128_kernel<KCV, 5, ScaleT>), grid, block, 0, st, p); \
+    else hipLaunchKernelGGL((gemv_b128_kernel<KCV, 7, ScaleT>), grid, block, 0, st, p);             \
+    return true;                                                                                   \
+  } while (0)
+  if (rpw == 0) return false;
+  switch ((p.K + 1023) / 1024) {
+    case 1: B(1);
+    case 2: B(2);
+    case 3: B(3);
+    case 4: B(4);
+    case 5: B(5);
+    case 6: B(6);
+    case 8: B(8);
+    case 9: B(9);
+    default: return false;
   }
-  if (need <= 5) {
-    switch (KC) {
-      case 1: L(1, 5); return true;
-      case 2: L(2, 5); return true;
-      case 3: L(3, 5); return true;
-      case 4: L(4, 5); return true;
-      default: return false;
-    }
+#undef B
+}
+
+template <typename ScaleT>
+bool try_mlp_b128(const QhMlpParams& p, hipStream_t st) {
+  if (p.K % 512 != 0) return false;
+  const int rpw = b128_rpw(p.N);
+  const dim3 grid(cu_count()), block(kB128Threads);
+#define B(KCV)                                                                                    \
+  do {                                                                                            \
+    if (rpw == 2) hipLaunchKernelGGL((mlp_b128_kernel<KCV, 2, ScaleT>), grid, block, 0, st, p);   \
+    else if (rpw == 5) hipLaunchKernelGGL((mlp_b128_kernel<KCV, 5, ScaleT>), grid, block, 0, st, p); \
+    else hipLaunchKernelGGL((mlp_b128_kernel<KCV, 7, ScaleT>), grid, block, 0, st, p);             \
+    return true;                                                                                  \
+  } while (0)
+  if (rpw == 0) return false;
+  switch ((p.K + 1023) / 1024) {
+    case 1: B(1);
+    case 2: B(2);
+    case 3: B(3);
+    case 4: B(4);
+    case 5: B(5);
+    case 6: B(6);
+    case 8: B(8);
+    case 9: B(9);
+    default: return false;
   }
-#undef L
-  return false;
+#undef B
 }
 
 template <int CPL, typename ScaleT>
@@ -1343,7 +1429,7 @@ int qh_launch_gemv(QhGemvParams p, bool scale_bf16, hipStream_t st) {
                  p.gnorm_d);
     return -1;
   }
-  if (fast && (scale_bf16 ? try_gemv_lds<uint16_t>(p, st) : try_gemv_lds<float>(p, st))) return 0;
+  if (fast && (scale_bf16 ? try_gemv_b128<uint16_t>(p, st) : try_gemv_b128<float>(p, st))) return 0;
   if (fast) {
 #define F(C) (scale_bf16 ? launch_gemv_fast_t<C, uint16_t>(p, st) : launch_gemv_fast_t<C, float>(p, st))
     QH_FAST_DISPATCH(p.K / 512, F)
@@ -1370,6 +1456,9 @@ int qh_launch_mlp(QhMlpParams p, bool scale_bf16, hipStream_t st) {
     qh_set_error("mlp: %d x %d exceeds 2^31 bytes", p.N, p.K);
     return -1;
   }
+  if (p.K % 512 == 0 && p.kb == p.K / 128 &&
+      (scale_bf16 ? try_mlp_b128<uint16_t>(p, st) : try_mlp_b128<float>(p, st)))
+    return 0;
   if (p.K % 512 == 0 && p.kb == p.K / 128) {
 #define F(C) (scale_bf16 ? launch_mlp_fast_t<C, uint16_t>(p, st) : launch_mlp_fast_t<C, float>(p, st))
     QH_FAST_DISPATCH(p.K / 512, F)
