@@ -77,7 +77,7 @@ def mlp_bytes(cfg):
 
 
 # The gate/up kernel the decode step launches (name as rocprofv3 reports it).
-GATE_UP_KERNEL = "mlp_fast_kernel<5, 1, float, 256>(QhMlpParams)"
+GATE_UP_KERNEL = "mlp_b128_kernel<3, 5, float>(QhMlpParams)"
 
 
 def measured_traffic():
@@ -340,7 +340,7 @@ def kernel_configs(eng, cpu=True):
         Wd = orc.dequant(w1, s1)
         cpu_t = {"dequant_matmul": _cpu_us(lambda: x1.float() @ orc.dequant(w1, s1).t()),
                  "matmul": _cpu_us(lambda: x1.float() @ Wd.t())}
-    entry("1 GEMV 9216x2560", "gemv_lds_kernel<3, 5, float, 2>", nbytes, us, n, cpu_t)
+    entry("1 GEMV 9216x2560", "gemv_b128_kernel<3, 5, float>", nbytes, us, n, cpu_t)
     del dw
 
     # ---- 2: decode MLP (norm + gate/up + SiLU*up, then down + residual) -------
@@ -373,7 +373,7 @@ def kernel_configs(eng, cpu=True):
             orc.mlp_decode(h, zero, ln, *m3)
         cpu_t = {"dequant_matmul": _cpu_us(mlp_dq),
                  "matmul": _cpu_us(lambda: orc.mlp_decode(h, zero, ln, *mats))}
-    entry("2 MLP gate/up 9216x2560 x2 + down 2560x9216", "mlp_fast_kernel<5, 1> + gemv_lds_kernel<9, 2, float, 1>",
+    entry("2 MLP gate/up 9216x2560 x2 + down 2560x9216", "mlp_b128_kernel<3, 5, float> + gemv_b128_kernel<9, 2, float>",
           nbytes, us, n, cpu_t)
     del sets
 
