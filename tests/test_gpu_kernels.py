@@ -92,8 +92,8 @@ def test_gemv_fp32_scales(N, K, mode):
     assert_close(y, ref, what=f"gemv {N}x{K} {mode}")
 
 
-# 2560 x 4096 and 4096 x 2560 (<= 48 KB of weights per CU) take the
-# LDS-streamed kernel, 9216 x 2560 the register pipeline.
+# 9216 x 2560, 2560 x 4096 and 4096 x 2560 take the 128-bit paced kernel with
+# bf16 scales (5, 2 and 2 row slots per wave); 256 x 384 the generic kernel.
 @pytest.mark.parametrize("N,K", [(256, 384), (9216, 2560), (2560, 4096), (4096, 2560)])
 def test_gemv_reference_abi_bf16_scales(N, K):
     """launch_gemv_v4_extern / v3 with bf16 scale_inv, via the reference-named wrapper."""
@@ -144,9 +144,9 @@ def test_grouped_projections_match_single():
     assert_close(uu, orc.linear(x.float(), orc.dequant(wk, sk.to(torch.bfloat16).float())), what="up")
 
 
-# (2560, 2560): the LDS-streamed kernel; the others the register pipeline
-# (one row group in flight for K = 9216, four for K = 2560).
-@pytest.mark.parametrize("N,K", [(2560, 2560), (2560, 9216), (12352, 2560)])
+# The first three take the 128-bit paced kernel (2, 2 and 7 row slots per
+# wave); 16384 x 2560 (8 slots per wave) falls back to the register pipeline.
+@pytest.mark.parametrize("N,K", [(2560, 2560), (2560, 9216), (12352, 2560), (16384, 2560)])
 def test_gemv_norm_prologue_and_residual_epilogue(N, K):
     g = gen(5)
     w, s = quant(g, N, K)
@@ -163,6 +163,31 @@ def test_gemv_norm_prologue_and_residual_epilogue(N, K):
     xn = orc.rmsnorm(x.float(), nw)
     ref = orc.bf16(res.float() + orc.linear(xn, orc.dequant(w, s)))
     assert_close(y, ref, atol_frac=1e-3, what="norm+gemv+res")
+
+
+# The 128-bit paced kernels take every K % 512 == 0 up to 9216 (KC = 1..9 one-KB
+# chunks per row, a half chunk when K % 1024 == 512) with 2, 5 or 7 row slots
+# per wave: 1, 33 and 50 rows per CU on a 256-CU part exercise each slot count,
+# with the (1+w) norm prologue and the residual epilogue.
+@pytest.mark.parametrize("K", [512, 1536, 2048, 3072, 4608, 6144, 8192, 9216])
+@pytest.mark.parametrize("rows_per_cu", [1, 33, 50])
+def test_gemv_b128_chunk_counts_and_slots(K, rows_per_cu):
+    g = gen(K + rows_per_cu)
+    N = rows_per_cu * 256 + 3
+    w, s = quant(g, N, K)
+    x = bf(randn(g, K))
+    nw = randn(g, K, std=0.02)
+    res = bf(randn(g, N))
+    lib = abi.load()
+    y = torch.empty(N, dtype=torch.bfloat16, device=DEV)
+    abi.check(lib.qh_gemv_e4m3(abi.ptr(cu(x)), None, abi.ptr(cu(nw)), 1e-6, K, abi.ptr(cu(res)),
+                               None, 1, abi.ptr(cu(w)), abi.ptr(cu(s)), abi.ptr(y), N, K // 128,
+                               None, None, None, 0, 0, None, None, None, 0, 0,
+                               None, None, None, 0, 0, 0, abi.stream_handle()))
+    sync()
+    xn = orc.rmsnorm(x.float(), nw)
+    ref = orc.bf16(res.float() + orc.linear(xn, orc.dequant(w, s)))
+    assert_close(y, ref, atol_frac=1e-3, what=f"b128 gemv {N}x{K}")
 
 
 def test_gemv_rejects_bad_args(lib):
@@ -220,7 +245,10 @@ def test_add_rmsnorm(M, D):
 
 
 # ------------------------------------------------------------------ MLP
-@pytest.mark.parametrize("H,I", [(2560, 9216), (256, 512)])
+# (2560, 16384): 64 gate/up pairs per CU, more than the 128-bit paced kernel's
+# 7 per wave, so the register pipeline runs gate/up, and down (K = 16384) the
+# generic kernel.
+@pytest.mark.parametrize("H,I", [(2560, 9216), (256, 512), (2560, 16384)])
 def test_mlp_decode(H, I):
     """fused (1+w) RMSNorm -> gate/up SiLU -> down (+residual)."""
     g = gen(2)
