@@ -1078,22 +1078,28 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(QhLmHeadParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = p.K;
   const int ngroups = (p.N + R - 1) / R;
-  const int stride = gridDim.x * 4;
   float best_v = -INFINITY;
   int best_i = 0x7fffffff;
 
   __shared__ __align__(16) uint16_t sx[CPL * 512];
   __shared__ float red[4];
-  int g = blockIdx.x * 4 + wid;
+  // Each wave streams a contiguous range of row groups (194.1 us for
+  // 248320 x 2560 on MI355X, against 196.4 us with groups dealt round-robin
+  // over the grid's waves).
+  const int nwaves = gridDim.x * 4;
+  const int per = (ngroups + nwaves - 1) / nwaves;
+  int g = (blockIdx.x * 4 + wid) * per;
+  const int gend = min(ngroups, g + per);
+  const int stride = 1;
   u32x4 wa[R][CPL];
-  if (g < ngroups) load_bf16_rows<CPL, R>(wa, p.w, p.N, g * R, K, lane);
+  if (g < gend) load_bf16_rows<CPL, R>(wa, p.w, p.N, g * R, K, lane);
   u32x4 xr[CPL];
   block_x_prologue<CPL>(xr, sx, red, p.x, nullptr, p.norm_w, p.eps, K);
 
-  while (g < ngroups) {
+  while (g < gend) {
     const int gn = g + stride;
     u32x4 wb[R][CPL];
-    if (gn < ngroups) load_bf16_rows<CPL, R>(wb, p.w, p.N, gn * R, K, lane);
+    if (gn < gend) load_bf16_rows<CPL, R>(wb, p.w, p.N, gn * R, K, lane);
     const int row0 = g * R;
     float acc[R];
 #pragma unroll
@@ -1492,6 +1498,8 @@ int qh_launch_read_stream(const void* src, uint64_t bytes, unsigned* out, int ou
 }
 
 int qh_lm_head_grid(int N) {
+  // 512 workgroups (two per CU): 768 and 1024 measured 200.3 and 208.6 us
+  // against 194.1 us.
   const int ng = (N + 3) / 4;
   return std::max(1, std::min(512, (ng + 3) / 4));
 }
