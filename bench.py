@@ -454,7 +454,7 @@ def kernel_configs(eng, cpu=True):
     nsplit = eng_mod.default_attn_splits(ms)
     caches = [(kc.to(dev), vc.to(dev)) for _ in range(n)]
     dq, dkn, dvn, dqn, dknw = (t.to(dev) for t in (q_all, kn, vn, qnw, knw))
-    scr = torch.empty(int(L.qh_attn_scratch_bytes(KV, nsplit, D)), dtype=torch.uint8, device=dev)
+    scr = torch.zeros(int(L.qh_attn_scratch_bytes(KV, nsplit, D)), dtype=torch.uint8, device=dev)
     cnt = torch.zeros(KV, dtype=torch.int32, device=dev)
     aout = torch.empty(H * D, dtype=bf, device=dev)
     att = [lambda k_=k_, v_=v_: abi.check(L.qh_attn_decode(

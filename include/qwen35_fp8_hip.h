@@ -179,7 +179,11 @@ int qh_rmsnorm(const void* x, const float* w, void* out, int rows, int D, float 
 int qh_add_rmsnorm(void* h, const void* o, const float* w, void* out, int rows, int D, float eps,
                    qh_stream_t stream);
 
-/* Scratch bytes for qh_attn_decode with nsplit > 1. */
+/* Scratch bytes for qh_attn_decode with nsplit > 1.  Layout (4-byte words):
+ * group arrival counters [n_kv][8], then the split records
+ * [n_kv][nsplit][8][head_dim + 2] and, above 8 splits, the level-2 records
+ * [n_kv][8][8][head_dim + 2] of the two-level merge.  The counters must be
+ * zero before the first call; the kernel returns them to zero itself. */
 size_t qh_attn_scratch_bytes(int n_kv_heads, int nsplit, int head_dim);
 
 /* Full-attention decode (layer_mid_attn + the sigmoid output gate of
@@ -196,11 +200,11 @@ int qh_attn_decode(const void* q, int q_stride, const void* gate, int gate_strid
  * and counters.  No counterpart in the reference; it is for callers that
  * cannot allocate (code under HIP graph capture, serving loops that forbid
  * hipMalloc): the split partials and arrival counters live in a fixed
- * library array (4 MiB + 256 bytes per GPU, held until the process ends).
+ * library array (8 MiB + 2304 bytes per GPU, held until the process ends).
  * Limits: n_kv <= 64, nsplit 1..64, n_heads / n_kv <= 8 and
- * n_kv * nsplit * 8 * (head_dim + 2) <= 2^20 partial floats, i.e.
- * qh_attn_scratch_bytes(n_kv, nsplit, head_dim) <= 4 MiB (partials are laid
- * out for up to 8 query heads per KV head); larger shapes return -1.  The first call on a device looks up the
+ * qh_attn_scratch_bytes(n_kv, nsplit, head_dim) <= 8 MiB (records are laid
+ * out for up to 8 query heads per KV head; at head_dim 256, 16 KV heads take
+ * up to 55 splits and 8 KV heads all 64); larger shapes return -1.  The first call on a device looks up the
  * array's address (make it outside graph capture).  Every call on one GPU
  * shares the array: calls that overlap on one GPU race. */
 int qh_attn_decode_noalloc(const void* q, int q_stride, const void* gate, int gate_stride,

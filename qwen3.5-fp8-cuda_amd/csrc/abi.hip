@@ -537,7 +537,9 @@ QH_EXPORT int qh_attn_decode(const void* q, int q_stride, const void* gate, int 
   a.slot = pos;
   a.total = pos + 1;
   a.nsplit = nsplit;
-  a.part = (float*)scratch;
+  // the scratch opens with the group counters [n_kv][8], then the records
+  a.gcounters = (unsigned*)scratch;
+  a.part = scratch ? (float*)scratch + (size_t)n_kv * 8 : nullptr;
   a.counters = counters;
   a.out = (uint16_t*)out;
   a.eps = eps;

@@ -180,6 +180,36 @@ __device__ __forceinline__ void norm_rope(float (&v)[D / 64], bool has_norm, con
   }
 }
 
+// Merges n <= 8 partial records (o [D] unnormalised against m, then m, l) at
+// base + r * stride, r < n: lane r holds record r's (m, l); the n o-vectors
+// are requested together (one memory round trip).  Returns the sum of the o
+// rescaled to the common maximum M, and L = sum of the l rescaled likewise.
+constexpr int kMergeBatch = 8;
+template <int NPL>
+__device__ __forceinline__ void merge_records(const float* base, size_t stride, int n, int lane,
+                                              float (&acc)[NPL], float& Mo, float& Lo) {
+  constexpr int D = NPL * 64;
+  const bool have = lane < n;
+  const float ls = have ? pub_load(base + lane * stride + D + 1) : 0.0f;
+  const float ms = have ? pub_load(base + lane * stride + D) : -INFINITY;
+  float part[kMergeBatch][NPL];
+#pragma unroll
+  for (int u = 0; u < kMergeBatch; ++u)
+    load_head_f32_coherent<NPL>(part[u], base + (size_t)u * stride, lane, u < n);
+  const float M = wave_max_dpp(ls > 0.0f ? ms : -INFINITY);
+  const float ws = ls > 0.0f ? __expf(ms - M) : 0.0f;
+  Lo = wave_total(ls * ws);
+  Mo = M;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kMergeBatch; ++u) {
+    const float w = __shfl(ws, u, 64);
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) acc[i] = w != 0.0f ? fmaf(part[u][i], w, acc[i]) : acc[i];
+  }
+}
+
 // HPW: query heads per wave, ceil(G / 4) for the GQA group size G.
 template <int D, int HPW>
 __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
@@ -438,62 +468,66 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(QhAttnParams p) {
       }
     }
   }
-  if (!arrive_last(p.counters + kvh, (unsigned)nactive, &s_last)) return;
+  // Up to 8 active splits: the last to arrive merges them all.  More: two
+  // levels, so no workgroup reads more than 8 records per query head (one
+  // reading all 64 splits' records through one CU took ~10 us at context
+  // 4096): the last split of each group of 8 merges its group into a
+  // level-2 record, and the last group merges the groups.
+  const size_t sstride = (size_t)MAXG * rec;
+  const float* src = p.part + (size_t)kvh * p.nsplit * sstride;  // records of this KV head
+  int nsrc = nactive;
+  if (nactive > kMergeBatch) {
+    const int grp = split / kMergeBatch, ngrp = (nactive + kMergeBatch - 1) / kMergeBatch;
+    const int gsize = min(kMergeBatch, nactive - grp * kMergeBatch);
+    float* lvl2 = p.part + (size_t)p.n_kv * p.nsplit * sstride + (size_t)kvh * kMergeBatch * sstride;
+    unsigned* gc = p.gcounters + kvh * kMergeBatch + grp;
+    if (!arrive_last(gc, (unsigned)gsize, &s_last)) return;
+#pragma unroll
+    for (int hi = 0; hi < HPW; ++hi) {
+      const int gi = wid + 4 * hi;
+      if (gi >= G) continue;
+      float acc[NPL], M, L;
+      merge_records<NPL>(src + (size_t)grp * kMergeBatch * sstride + (size_t)gi * rec, sstride, gsize, lane,
+                         acc, M, L);
+      float* dst = lvl2 + (size_t)grp * sstride + (size_t)gi * rec;
+      store_head_f32_coherent<NPL>(dst, lane, acc);
+      if (lane == 0) {
+        pub_store(dst + D, M);
+        pub_store(dst + D + 1, L);
+      }
+    }
+    if (threadIdx.x == 0) reset_counter(gc);
+    if (!arrive_last(p.counters + kvh, (unsigned)ngrp, &s_last)) return;
+    src = lvl2;
+    nsrc = ngrp;
+  } else if (!arrive_last(p.counters + kvh, (unsigned)nactive, &s_last)) {
+    return;
+  }
 #pragma unroll
   for (int hi = 0; hi < HPW; ++hi) {
     const int gi = wid + 4 * hi;
     if (gi >= G) continue;
-    const float* base = p.part + ((size_t)kvh * p.nsplit * MAXG + gi) * rec;
-    const size_t sstride = (size_t)MAXG * rec;
-    // lane s holds split s's (m, l); nsplit <= 64 (checked on the host)
-    const bool have = lane < nactive;
-    const float ls = have ? pub_load(base + lane * sstride + D + 1) : 0.0f;
-    const float ms = have ? pub_load(base + lane * sstride + D) : -INFINITY;
-    // The partials of MB splits are requested together (one memory round trip
-    // per batch, not per split; the first batch travels with the (m, l)
-    // loads); slots past the last active split load zeros.  (A 16-wide batch
-    // above 8 active splits measured no faster.)
-    constexpr int MB = 8;
-    float part[MB][NPL];
-#pragma unroll
-    for (int u = 0; u < MB; ++u)
-      load_head_f32_coherent<NPL>(part[u], base + (size_t)u * sstride, lane, u < nactive);
-    const float M = wave_max_dpp(ls > 0.0f ? ms : -INFINITY);
-    const float ws = ls > 0.0f ? __expf(ms - M) : 0.0f;
-    const float L = wave_total(ls * ws);
-    float acc[NPL];
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) acc[i] = 0.0f;
-    for (int s0 = 0; s0 < nactive; s0 += MB) {
-      if (s0 > 0) {
-#pragma unroll
-        for (int u = 0; u < MB; ++u)
-          load_head_f32_coherent<NPL>(part[u], base + (size_t)(s0 + u) * sstride, lane, s0 + u < nactive);
-      }
-#pragma unroll
-      for (int u = 0; u < MB; ++u) {
-        const float w = __shfl(ws, s0 + u, 64);  // s0 + u < 64: nsplit <= 64
-#pragma unroll
-        for (int i = 0; i < NPL; ++i) acc[i] = w != 0.0f ? fmaf(part[u][i], w, acc[i]) : acc[i];
-      }
-    }
+    float acc[NPL], M, L;
+    merge_records<NPL>(src + (size_t)gi * rec, sstride, nsrc, lane, acc, M, L);
     emit(gi, gate_v[hi], acc, 1.0f / L);
   }
   if (threadIdx.x == 0) reset_counter(p.counters + kvh);
 }
 
 // ---- fixed scratch of qh_attn_decode_noalloc --------------------------------
-// Words [0, kStaticCounterWords) are the per-KV-head arrival counters (the
-// kernel's last arriver returns each to zero), the rest the split partials.
+// Words [0, kStaticCounterWords) are the per-KV-head arrival counters and
+// then the group counters [64][8] of the two-level merge (the kernel's last
+// arrivers return each to zero), the rest the split partials.
 // The array is device memory that each GPU the library runs on holds until
 // the process ends; every call on one GPU shares it.
-constexpr int kStaticCounterWords = 64;                       // n_kv <= 64
-constexpr size_t kStaticPartFloats = (size_t)1 << 20;         // 4 MiB of partials
+constexpr int kStaticKv = 64;                                 // n_kv <= 64
+constexpr int kStaticCounterWords = kStaticKv * (1 + kMergeBatch);
+constexpr size_t kStaticPartFloats = (size_t)1 << 21;         // 8 MiB of partials
 constexpr size_t kStaticWords = kStaticCounterWords + kStaticPartFloats;
 constexpr int kMaxDevices = 64;
 
 __global__ __launch_bounds__(64) void zero_words_kernel(unsigned* w, int n) {
-  if ((int)threadIdx.x < n) w[threadIdx.x] = 0u;
+  for (int i = (int)threadIdx.x; i < n; i += 64) w[i] = 0u;
 }
 
 }  // namespace
@@ -532,8 +566,13 @@ uint32_t* static_scratch(hipStream_t st) {
 
 }  // namespace
 
+// Layout (4-byte words): the group arrival counters of the two-level merge
+// [n_kv][8] (zero before the first call; they return to zero themselves),
+// the splits' records [n_kv][nsplit][MAXG][D + 2] and, above 8 splits, the
+// level-2 records [n_kv][8][MAXG][D + 2].
 size_t qh_attn_scratch_floats(int n_kv, int nsplit, int head_dim) {
-  return (size_t)n_kv * nsplit * MAXG * (head_dim + 2);
+  const size_t rec = (size_t)MAXG * (head_dim + 2);
+  return (size_t)n_kv * kMergeBatch + (size_t)n_kv * (nsplit + (nsplit > kMergeBatch ? kMergeBatch : 0)) * rec;
 }
 
 int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
@@ -552,7 +591,8 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
     qh_set_error("attn: rotary_dim=%d unsupported for head_dim=%d", p.rot, head_dim);
     return -1;
   }
-  if (p.nsplit < 1 || p.nsplit > 64 || (p.nsplit > 1 && (!p.part || !p.counters))) {
+  if (p.nsplit < 1 || p.nsplit > 64 || (p.nsplit > 1 && (!p.part || !p.counters)) ||
+      (p.nsplit > kMergeBatch && !p.gcounters)) {
     qh_set_error("attn: nsplit=%d must be 1..64; split-K needs scratch and counters", p.nsplit);
     return -1;
   }
@@ -579,8 +619,8 @@ int qh_launch_attn(const QhAttnParams& p, int head_dim, hipStream_t st) {
 // counters live in the file-scope array above instead of caller memory.  No
 // counterpart in the reference; for callers that cannot allocate (code under
 // graph capture, serving loops that forbid hipMalloc).  Limits: n_kv <= 64
-// and qh_attn_scratch_floats = n_kv * nsplit * MAXG * (head_dim + 2) <= 2^20
-// partial floats (4 MiB).
+// and qh_attn_scratch_floats(n_kv, nsplit, head_dim) <= 2^21 (8 MiB): the
+// split records, plus the level-2 records above 8 splits.
 // Calls that overlap on one GPU race on the shared array.
 extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
     const void* q, int q_stride, const void* gate, int gate_stride, const void* k_new,
@@ -588,12 +628,13 @@ extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
     const float* sin_t, void* k_cache, void* v_cache, int max_seq, int head_dim, int rot,
     int n_heads, int n_kv, const int* pos_dev, int pos, int nsplit, void* out, float eps,
     hipStream_t stream) {
-  if (n_kv < 1 || n_kv > kStaticCounterWords || nsplit < 1 || nsplit > 64 ||
+  if (n_kv < 1 || n_kv > kStaticKv || nsplit < 1 || nsplit > 64 ||
       (head_dim != 128 && head_dim != 256) ||
       qh_attn_scratch_floats(n_kv, nsplit, head_dim) > kStaticPartFloats) {
     qh_set_error("qh_attn_decode_noalloc: n_kv=%d, nsplit=%d, head_dim=%d exceed the fixed "
-                 "scratch (n_kv <= %d, nsplit 1..64, n_kv*nsplit*%d*(head_dim+2) <= %zu floats)",
-                 n_kv, nsplit, head_dim, kStaticCounterWords, MAXG, kStaticPartFloats);
+                 "scratch (n_kv <= %d, nsplit 1..64, qh_attn_scratch_floats <= %zu floats: "
+                 "n_kv*nsplit*%d*(head_dim+2), plus n_kv*8*%d*(head_dim+2)+n_kv*8 above 8 splits)",
+                 n_kv, nsplit, head_dim, kStaticKv, kStaticPartFloats, MAXG, MAXG);
     return -1;
   }
   uint32_t* ws = static_scratch(stream);
@@ -622,6 +663,7 @@ extern "C" __attribute__((visibility("default"))) int qh_attn_decode_noalloc(
   a.total = pos + 1;
   a.nsplit = nsplit;
   a.counters = (unsigned*)ws;
+  a.gcounters = (unsigned*)ws + kStaticKv;
   a.part = (float*)(ws + kStaticCounterWords);
   a.out = (uint16_t*)out;
   a.eps = eps;

@@ -29,8 +29,9 @@ struct QhAttnParams {
   int slot;
   int total;
   int nsplit;               // position splits per KV head (1 = no scratch needed)
-  float* part;              // scratch, qh_attn_scratch_floats() floats
+  float* part;              // split records, then the level-2 records (nsplit > 8)
   unsigned* counters;       // [n_kv] zero-initialised arrival counters
+  unsigned* gcounters;      // [n_kv][8] zero-initialised group counters (nsplit > 8)
   uint16_t* out;            // [n_heads, D] bf16
   float eps;
 };

@@ -19,11 +19,13 @@ def _args(q_all, k_new, v_new, qn, kn, cos, sin, kc, vc, max_seq, D, rot, Hq, Hk
             max_seq, D, rot, Hq, Hkv, None, pos, nsplit]
 
 
-# (Hq, Hkv, D, ctx, max_seq, nsplit) of the two calls.  8 KV heads x 63 splits
-# x 8 x 258 = 1,040,256 partial floats is the largest head_dim-256 shape at 8
-# KV heads that fits the fixed 2^20-float array.
+# (Hq, Hkv, D, ctx, max_seq, nsplit) of the two calls.  At head_dim 256, 16 KV
+# heads x (55 split + 8 level-2 records) x 8 x 258 floats + 16 x 8 counters =
+# 2,080,640 words is the largest 16-KV-head shape that fits the fixed 2^21-float
+# array; 55 splits also leave a ragged last merge group (7 of 8).
 @pytest.mark.parametrize("first,second", [((16, 4, 256, 4096, 4096, 64), (8, 2, 128, 300, 512, 16)),
-                                          ((32, 8, 256, 4096, 4096, 63), (16, 4, 256, 700, 1024, 8))])
+                                          ((64, 16, 256, 4096, 4096, 55), (16, 4, 256, 700, 1024, 8)),
+                                          ((32, 8, 256, 4096, 4096, 64), (16, 4, 256, 700, 1024, 12))])
 def test_noalloc_attention_matches_scratch_entry_point(first, second):
     lib = abi.load()
     for step, (Hq, Hkv, D, ctx, max_seq, nsplit) in enumerate((first, second)):
@@ -58,12 +60,14 @@ def test_noalloc_attention_matches_scratch_entry_point(first, second):
         assert_close(outs[1], ref, atol_frac=1e-3, what=f"noalloc attention, call {step}")
 
 
-@pytest.mark.parametrize("n_kv,nsplit", [(64, 64), (8, 64)])
+@pytest.mark.parametrize("n_kv,nsplit", [(64, 64), (16, 56)])
 def test_noalloc_attention_rejects_shapes_beyond_its_scratch(n_kv, nsplit):
-    """n_kv x nsplit x 8 x (256 + 2) floats above 2^20 (8 x 64: 1,056,768, one
-    split more than the accepted 8 x 63) is refused before any launch."""
+    """A shape whose scratch is above 2^21 words (16 x 56: 16 x 8 + 16 x 64 x
+    8 x 258 = 2,113,664, one split more than the accepted 16 x 55) is refused
+    before any launch."""
     lib = abi.load()
-    assert lib.qh_attn_scratch_bytes(n_kv, nsplit, 256) > 4 << 20
+    assert lib.qh_attn_scratch_bytes(n_kv, nsplit, 256) > 8 << 20
+    assert lib.qh_attn_scratch_bytes(16, 55, 256) <= 8 << 20
     x = torch.zeros(16, dtype=torch.bfloat16, device=DEV)
     rc = lib.qh_attn_decode_noalloc(abi.ptr(x), 512, None, 0, abi.ptr(x), abi.ptr(x), None, None,
                                     None, None, abi.ptr(x), abi.ptr(x), 4096, 256, 64, 4 * n_kv, n_kv,
