@@ -211,7 +211,11 @@ __device__ __forceinline__ float qh_sigmoid(float x) { return 1.0f / (1.0f + exp
 __device__ __forceinline__ float qh_silu(float x) { return x / (1.0f + expf(-x)); }
 // SiLU on the fast exponential, for per-element loops on a kernel's critical
 // path (the gated RMSNorm prologue of the decode output projection).
-__device__ __forceinline__ float qh_silu_fast(float x) { return x / (1.0f + __expf(-x)); }
+// The reciprocal is the hardware v_rcp_f32 (about 1 ulp) in place of the IEEE
+// division's ten-instruction sequence; callers round the result to bf16.
+__device__ __forceinline__ float qh_silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 // torch.nn.functional.softplus(beta=1, threshold=20)
 __device__ __forceinline__ float qh_softplus(float x) {
   return x > 20.0f ? x : log1pf(expf(x));

@@ -309,10 +309,13 @@ def _attn_case(g, ctx, Hq=16, Hkv=4, D=256, rot=64, max_seq=None):
 
 
 # (4096, 64), (2049, 64), (300, 64): the engine's split count for a 4096-slot
-# cache (engine.default_attn_splits), where the merge's lanes 32-63 carry
-# (m, l) pairs and the partials arrive in eight batches.
+# cache (engine.default_attn_splits).  Above 8 active splits the merge runs in
+# two levels (groups of 8, then the group records): 4096/64 has 8 full groups,
+# 2049/64 33 active splits (a last group of 1), 300/64 and 427/32 10 and 14
+# (8 + 2, 8 + 6), 288/64 9 (8 + 1), 512/64 16 (8 + 8), 545/64 18 (8 + 8 + 2).
 @pytest.mark.parametrize("ctx,splits", [(1, 1), (17, 1), (130, 4), (4096, 32), (427, 32),
-                                        (4096, 64), (2049, 64), (300, 64)])
+                                        (4096, 64), (2049, 64), (300, 64), (288, 64), (512, 64),
+                                        (545, 64)])
 def test_attn_decode(ctx, splits):
     """BASELINE config 4b (ctx 4096): q/k norm, partial RoPE (theta 1e7, 64 of
     256 dims), KV write at slot ctx-1, GQA 16/4, sigmoid gate."""
