@@ -160,6 +160,21 @@ def test_validation_errors_need_no_gpu():
     assert "multiple of 8" in abi.last_error()
 
 
+def test_attention_scratch_layout():
+    """qh_attn_scratch_bytes: n_kv x 8 group-counter words, then the split
+    records [n_kv][nsplit][8][D + 2] and, above 8 splits, the level-2 records
+    [n_kv][8][8][D + 2] (4-byte words).  Split-K with no scratch, and more than
+    8 splits with scratch but no room for the group counters, are refused."""
+    lib = abi.load()
+    for n_kv, nsplit, D in [(4, 1, 256), (4, 8, 256), (4, 9, 256), (4, 64, 256), (2, 16, 128), (16, 55, 256)]:
+        words = n_kv * 8 + n_kv * (nsplit + (8 if nsplit > 8 else 0)) * 8 * (D + 2)
+        assert lib.qh_attn_scratch_bytes(n_kv, nsplit, D) == 4 * words, (n_kv, nsplit, D)
+    rc = lib.qh_attn_decode(None, 512, None, 512, None, None, None, None, None, None, None, None,
+                            4096, 256, 64, 16, 4, None, 100, 16, None, ctypes.c_void_p(4096), None, 1e-6,
+                            None)
+    assert rc == -1 and "scratch" in abi.last_error()
+
+
 def test_scale_mode_encoding():
     import torch
     w = torch.zeros(256, 512, dtype=torch.uint8)
