@@ -17,7 +17,9 @@
 // the GQA group, so each KV head is read from HBM exactly once per step.  Each
 // split keeps an online-softmax state; the last split to finish for a KV head
 // (atomic arrival counter, self-resetting) merges the partial states and
-// applies the output gate.  The new token's K/V come from registers, so no
+// applies the output gate.  Above 8 active splits the merge has two levels:
+// the last arriver of each group of 8 splits merges its group, the last group
+// merges the group records.  The new token's K/V come from registers, so no
 // split ever waits on another.
 #include <cstring>
 #include <mutex>
