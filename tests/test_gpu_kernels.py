@@ -367,6 +367,8 @@ def _check_attn_decode(ctx, splits, Hq, Hkv):
         assert torch.equal(kcg[:, pos].cpu().float(), kc_ref[:, pos]), "K cache slot"
         assert torch.equal(vcg[:, pos].cpu().float(), vc_ref[:, pos]), "V cache slot"
         assert int(counters.abs().sum()) == 0, "arrival counters must self-reset"
+        # the two-level merge's group counters open the scratch ([Hkv][8] words)
+        assert int(scratch[:Hkv * 8 * 4].abs().sum()) == 0, "group counters must self-reset"
 
 
 def test_layer_mid_attn_reference_abi():
